@@ -1,0 +1,318 @@
+// C ABI of libfa_gfx950.so (declared in include/fa_gfx950.h): argument validation, kernel
+// selection from the registries of built instantiations, and launches on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "fa_kernels.h"
+#include "../../include/fa_gfx950.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return FA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+const fa::FaKernelEntry* find_fwd(int stages, int dtype, int D, int waves, int rows_per_wave, int block_n,
+                                  int split) {
+  int n = 0;
+  const fa::FaKernelEntry* e = fa::fa_fwd_registry(&n);
+  for (int i = 0; i < n; ++i)
+    if (e[i].stages == stages && e[i].dtype == dtype && e[i].D == D && e[i].waves == waves &&
+        e[i].rows_per_wave == rows_per_wave && e[i].block_n == block_n && e[i].split == split)
+      return &e[i];
+  return nullptr;
+}
+
+const fa::FaMergeEntry* find_merge(int dtype, int D) {
+  int n = 0;
+  const fa::FaMergeEntry* e = fa::fa_merge_registry(&n);
+  for (int i = 0; i < n; ++i)
+    if (e[i].dtype == dtype && e[i].D == D) return &e[i];
+  return nullptr;
+}
+
+const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
+  int n = 0;
+  const fa::GemmKernelEntry* e = fa::gemm_registry(&n);
+  for (int i = 0; i < n; ++i)
+    if (e[i].block_m == t->block_m && e[i].block_n == t->block_n && e[i].block_k == t->block_k &&
+        e[i].waves == t->waves)
+      return &e[i];
+  return nullptr;
+}
+
+int stages_of(int variant) { return variant == FA_VARIANT_BASIC ? 1 : 2; }
+
+// Resolve (variant, tile) to the main kernel; nullptr + message when not built.
+const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_tile* t, bool* split_out,
+                                     int* code) {
+  *code = FA_OK;
+  if (variant < FA_VARIANT_BASIC || variant > FA_VARIANT_SLICED) {
+    *code = fail(FA_EINVAL, "unknown attention variant %d", variant);
+    return nullptr;
+  }
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16) {
+    *code = fail(FA_ENOTSUP, "unsupported dtype code %d (fp16=0, bf16=1)", dtype);
+    return nullptr;
+  }
+  if (D != 64 && D != 128 && D != 256) {
+    *code = fail(FA_ENOTSUP, "head dim D=%d is not built (64, 128, 256)", D);
+    return nullptr;
+  }
+  if (t == nullptr || t->waves <= 0 || t->block_m <= 0 || t->block_m % t->waves != 0) {
+    *code = fail(FA_EINVAL, "invalid attention tile");
+    return nullptr;
+  }
+  const int splits = t->splits < 1 ? 1 : t->splits;
+  if (variant != FA_VARIANT_SLICED && splits != 1) {
+    *code = fail(FA_EINVAL, "splits=%d requires the sliced variant", splits);
+    return nullptr;
+  }
+  const bool split = splits > 1;
+  *split_out = split;
+  const fa::FaKernelEntry* e =
+      find_fwd(stages_of(variant), dtype, D, t->waves, t->block_m / t->waves, t->block_n, split ? 1 : 0);
+  if (e == nullptr)
+    *code = fail(FA_ENOTSUP,
+                 "attention tile block_m=%d block_n=%d waves=%d stages=%d split=%d is not built for "
+                 "dtype=%d D=%d",
+                 t->block_m, t->block_n, t->waves, stages_of(variant), split ? 1 : 0, dtype, D);
+  return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_last_error(void) { return g_last_error.c_str(); }
+
+int64_t fa_fwd_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t D, int32_t splits) {
+  if (splits <= 1 || B <= 0 || H <= 0 || M <= 0 || D <= 0) return 0;
+  const int64_t rows = (int64_t)splits * B * H * M;
+  const int64_t o_bytes = rows * D * 4;
+  const int64_t lse_off = (o_bytes + 255) & ~(int64_t)255;
+  return lse_off + rows * 4;
+}
+
+int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile) {
+  bool split = false;
+  int code = FA_OK;
+  const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
+  if (e == nullptr) return code;
+  if (split && find_merge(dtype, D) == nullptr) return fail(FA_ENOTSUP, "no merge kernel for D=%d", D);
+  return ok();
+}
+
+int fa_fwd(const fa_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(FA_EINVAL, "null argument block");
+  bool split = false;
+  int code = FA_OK;
+  const fa::FaKernelEntry* e = resolve_fwd(a->variant, a->dtype, a->D, &a->tile, &split, &code);
+  if (e == nullptr) return code;
+  if (a->B < 0 || a->H <= 0 || a->H_kv <= 0 || a->M < 0 || a->N < 0)
+    return fail(FA_EINVAL, "invalid sizes B=%d H=%d H_kv=%d M=%d N=%d", a->B, a->H, a->H_kv, a->M, a->N);
+  if (a->H % a->H_kv != 0)
+    return fail(FA_EINVAL, "query heads H=%d must be a multiple of kv heads H_kv=%d", a->H, a->H_kv);
+  if (a->B == 0 || a->M == 0) return ok();  // nothing to compute
+  if (!a->q || !a->k || !a->v || !a->o) return fail(FA_EINVAL, "null q/k/v/o pointer");
+  if (a->q_stride[3] != 1 || a->k_stride[3] != 1 || a->v_stride[3] != 1 || a->o_stride[3] != 1)
+    return fail(FA_EINVAL, "head-dim stride must be 1 for q, k, v and o");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+    return fail(FA_EINVAL, "q, k, v and o must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if (a->q_stride[i] % 8 || a->k_stride[i] % 8 || a->v_stride[i] % 8 || a->o_stride[i] % 4)
+      return fail(FA_EINVAL, "row strides must keep 16-byte alignment (q/k/v multiple of 8, o of 4 elements)");
+  if (!std::isfinite(a->sm_scale) || a->sm_scale <= 0.f)
+    return fail(FA_EINVAL, "sm_scale must be positive and finite, got %g", (double)a->sm_scale);
+
+  const int bm = a->tile.block_m, bn = a->tile.block_n;
+  const int splits = a->tile.splits < 1 ? 1 : a->tile.splits;
+  const int64_t m_blocks = (a->M + bm - 1) / bm;
+  const int64_t n_tiles = a->N > 0 ? (a->N + bn - 1) / bn : 1;
+  const int64_t tiles_per_split = (n_tiles + splits - 1) / splits;
+  const int64_t total = m_blocks * a->B * a->H * splits;
+  if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large (%lld workgroups)", (long long)total);
+
+  fa::FwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.lse = a->lse;
+  p.sq0 = a->q_stride[0]; p.sq1 = a->q_stride[1]; p.sq2 = a->q_stride[2];
+  p.sk0 = a->k_stride[0]; p.sk1 = a->k_stride[1]; p.sk2 = a->k_stride[2];
+  p.sv0 = a->v_stride[0]; p.sv1 = a->v_stride[1]; p.sv2 = a->v_stride[2];
+  p.so0 = a->o_stride[0]; p.so1 = a->o_stride[1]; p.so2 = a->o_stride[2];
+  p.sl0 = a->lse_stride[0]; p.sl1 = a->lse_stride[1]; p.sl2 = a->lse_stride[2];
+  p.B = a->B; p.H = a->H; p.Hkv = a->H_kv; p.M = a->M; p.N = a->N;
+  p.group = a->H / a->H_kv;
+  p.sm_scale = a->sm_scale;
+  p.c = a->sm_scale * 1.4426950408889634f;
+  p.causal = a->causal ? 1 : 0;
+  p.splits = splits;
+  p.tiles_per_split = (int32_t)tiles_per_split;
+  p.m_blocks = (int32_t)m_blocks;
+  p.total_blocks = (int32_t)total;
+
+  const fa::FaMergeEntry* me = nullptr;
+  if (split) {
+    me = find_merge(a->dtype, a->D);
+    if (me == nullptr) return fail(FA_ENOTSUP, "no merge kernel for D=%d", a->D);
+    const int64_t need = fa_fwd_workspace_bytes(a->B, a->H, a->M, a->D, splits);
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+      return fail(FA_EWORKSPACE, "split-KV workspace of %lld bytes needed, got %lld", (long long)need,
+                  (long long)a->workspace_bytes);
+    if (!aligned16(a->workspace)) return fail(FA_EINVAL, "workspace must be 16-byte aligned");
+    const int64_t rows = (int64_t)splits * a->B * a->H * a->M;
+    p.ws_o = static_cast<float*>(a->workspace);
+    p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + ((rows * a->D * 4 + 255) & ~(int64_t)255));
+  }
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* kargs[] = {&p};
+  hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0, s);
+  if (err != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(err));
+
+  if (split) {
+    fa::MergeParams mp;
+    mp.ws_o = p.ws_o;
+    mp.ws_lse = p.ws_lse;
+    mp.o = p.o;
+    mp.lse = a->lse;
+    mp.so0 = p.so0; mp.so1 = p.so1; mp.so2 = p.so2;
+    mp.sl0 = p.sl0; mp.sl1 = p.sl1; mp.sl2 = p.sl2;
+    mp.B = a->B; mp.H = a->H; mp.M = a->M; mp.splits = splits;
+    const int64_t rows = (int64_t)a->B * a->H * a->M;
+    const int64_t blocks = (rows + 3) / 4;
+    if (blocks > 0x7fffffffLL) return fail(FA_EINVAL, "merge grid too large");
+    void* margs[] = {&mp};
+    err = hipLaunchKernel(me->fn, dim3((unsigned)blocks), dim3(256), margs, 0, s);
+    if (err != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(err));
+  }
+  return ok();
+}
+
+int gemm_f16_supported(const gemm_tile* tile) {
+  if (tile == nullptr) return fail(FA_EINVAL, "null gemm tile");
+  if (find_gemm(tile) == nullptr)
+    return fail(FA_ENOTSUP, "gemm tile %dx%dx%d with %d waves is not built", tile->block_m, tile->block_n,
+                tile->block_k, tile->waves);
+  return ok();
+}
+
+int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_t K, int64_t lda, int64_t ldb,
+             int64_t ldc, const gemm_tile* tile, void* stream) {
+  if (tile == nullptr) return fail(FA_EINVAL, "null gemm tile");
+  const fa::GemmKernelEntry* e = find_gemm(tile);
+  if (e == nullptr)
+    return fail(FA_ENOTSUP, "gemm tile %dx%dx%d with %d waves is not built", tile->block_m, tile->block_n,
+                tile->block_k, tile->waves);
+  if (M < 0 || N < 0 || K < 0) return fail(FA_EINVAL, "negative GEMM size");
+  if (M == 0 || N == 0) return ok();
+  if (K == 0) return fail(FA_EINVAL, "K=0 is not supported (the reference requires K %% 32 == 0, K > 0)");
+  if (M % e->block_m || N % e->block_n || K % e->block_k)
+    return fail(FA_EINVAL, "M=%d N=%d K=%d must be multiples of the %dx%dx%d tile", M, N, K, e->block_m,
+                e->block_n, e->block_k);
+  if (!a || !b || !c) return fail(FA_EINVAL, "null GEMM pointer");
+  if (!aligned16(a) || !aligned16(b) || (reinterpret_cast<uintptr_t>(c) & 7u))
+    return fail(FA_EINVAL, "A and B must be 16-byte aligned, C 8-byte aligned");
+  if (lda < K || ldb < N || ldc < N || lda % 8 || ldb % 8 || ldc % 4)
+    return fail(FA_EINVAL, "leading dimensions lda=%lld ldb=%lld ldc=%lld invalid", (long long)lda,
+                (long long)ldb, (long long)ldc);
+  if (tile->group_m < 1) return fail(FA_EINVAL, "group_m must be >= 1");
+  fa::GemmParams p;
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.c = static_cast<uint16_t*>(c);
+  p.M = M; p.N = N; p.K = K;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.group_m = tile->group_m;
+  p.tiles_m = M / e->block_m;
+  p.tiles_n = N / e->block_n;
+  const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
+  if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large");
+  void* kargs[] = {&p};
+  hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0,
+                                   static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FA_EHIP, "gemm launch failed: %s", hipGetErrorString(err));
+  return ok();
+}
+
+int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
+                        const gemm_tile* gtile, fa_resources* out) {
+  if (out == nullptr) return fail(FA_EINVAL, "null output");
+  const void* fn = nullptr;
+  int threads = 0;
+  if (op == 0) {
+    bool split = false;
+    int code = FA_OK;
+    const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
+    if (e == nullptr) return code;
+    fn = e->fn;
+    threads = e->waves * 64;
+  } else if (op == 1) {
+    if (gtile == nullptr) return fail(FA_EINVAL, "null gemm tile");
+    const fa::GemmKernelEntry* e = find_gemm(gtile);
+    if (e == nullptr) return fail(FA_ENOTSUP, "gemm tile not built");
+    fn = e->fn;
+    threads = e->waves * 64;
+  } else {
+    return fail(FA_EINVAL, "unknown op %d", op);
+  }
+  hipFuncAttributes attr;
+  std::memset(&attr, 0, sizeof(attr));
+  hipError_t err = hipFuncGetAttributes(&attr, fn);
+  if (err != hipSuccess) return fail(FA_EHIP, "hipFuncGetAttributes failed: %s", hipGetErrorString(err));
+  out->vgprs = attr.numRegs;
+  out->agprs = -1;
+  out->sgprs = -1;
+  out->lds_bytes = (int32_t)attr.sharedSizeBytes;
+  out->scratch_bytes = (int32_t)attr.localSizeBytes;
+  out->threads = threads;
+  out->max_threads = attr.maxThreadsPerBlock;
+  return ok();
+}
+
+int fa_device_limits(int32_t device, fa_device_limits_t* out) {
+  if (out == nullptr) return fail(FA_EINVAL, "null output");
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return fail(FA_EHIP, "hipGetDeviceProperties failed: %s", hipGetErrorString(err));
+  out->lds_bytes_per_cu = (int32_t)prop.maxSharedMemoryPerMultiProcessor;
+  out->registers_per_simd = 512 * 64;
+  out->register_file_bytes_per_simd = 512 * 64 * 4;
+  out->wavefront_size = prop.warpSize;
+  out->max_threads_per_block = prop.maxThreadsPerBlock;
+  out->cu_count = prop.multiProcessorCount;
+  out->clock_khz = prop.clockRate;
+  int arch = 0;
+  if (std::sscanf(prop.gcnArchName, "gfx%d", &arch) != 1) arch = 0;
+  out->gcn_arch = arch;
+  return ok();
+}
+
+}  // extern "C"

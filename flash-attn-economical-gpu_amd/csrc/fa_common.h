@@ -1,0 +1,92 @@
+// Device-side helpers shared by the attention and GEMM kernels (gfx950 / CDNA4 only).
+//
+// MFMA fragment conventions used throughout (v_mfma_f32_32x32x16_{f16,bf16}, wave64):
+//   lane l, col = l & 31, half = l >> 5
+//   A operand (32 x 16): lane holds row `col`, k-slots 8*half .. 8*half+7   (8 x 16-bit)
+//   B operand (16 x 32): lane holds column `col`, k-slots 8*half .. 8*half+7 (8 x 16-bit)
+//   C/D (32 x 32 fp32): lane holds column `col`, register r holds row 8*(r/4) + 4*half + (r%4)
+// The hardware pairs A's and B's k-slots identically, so any permutation of the 16 k values that
+// is applied to both operands leaves the product unchanged; the kernels rely on that.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct f16_t {};   // tag: IEEE binary16 storage
+struct bf16_t {};  // tag: bfloat16 storage
+
+template <typename Tag>
+struct DT;
+
+template <>
+struct DT<f16_t> {
+  typedef half8 vec8;
+  __device__ static inline floatx16 mfma32(const u32x4& a, const u32x4& b, const floatx16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  }
+  // Two fp32 -> packed pair of binary16 (round to nearest even), low half = x.
+  __device__ static inline uint32_t pack2(float x, float y) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 v;
+    v[0] = (_Float16)x;
+    v[1] = (_Float16)y;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline float to_float(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+};
+
+template <>
+struct DT<bf16_t> {
+  typedef bf16x8 vec8;
+  __device__ static inline floatx16 mfma32(const u32x4& a, const u32x4& b, const floatx16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float x, float y) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    b2 v;
+    v[0] = (__bf16)x;
+    v[1] = (__bf16)y;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline float to_float(uint16_t bits) {
+    return __uint_as_float(((uint32_t)bits) << 16);
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+};
+
+// Value of x in lane (l ^ 32), through the LDS crossbar (ds_bpermute).
+__device__ inline float xhalf(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup id remapped so that consecutive logical ids land on the same XCD. Workgroups are
+// dispatched round-robin over the 8 XCDs of MI355X; logical id L = xcd * per + slot keeps
+// neighbouring tiles (which share K/V or A/B panels) inside one XCD's L2.
+__device__ inline int xcd_remap(int pid, int total) {
+  constexpr int kXcds = 8;
+  if (total % kXcds != 0) return pid;
+  const int per = total / kXcds;
+  return (pid % kXcds) * per + (pid / kXcds);
+}
+
+}  // namespace fa

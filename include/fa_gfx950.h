@@ -1,0 +1,150 @@
+/*
+ * fa_gfx950.h -- C ABI of libfa_gfx950.so, the MI355X (gfx950 / CDNA4) FlashAttention-forward
+ * and fp16 GEMM library.
+ *
+ * Every entry point is plain C: pointers, fixed-width integers and floats, no HIP or torch types.
+ * Device pointers come from the caller (PyTorch allocates every buffer, including the split-KV
+ * workspace); the library never allocates or frees device memory. `stream` is a hipStream_t
+ * passed as void* (the caller's current stream); no entry point synchronises the host.
+ *
+ * Return value of every int-returning entry point: FA_OK (0) or one of the FA_E* codes below;
+ * fa_last_error() then gives a thread-local message.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   fa_fwd(variant=FA_VARIANT_BASIC)   <- _flash_attn_fwd_kernel_basic[grid](...)          flash_atten.py:14-50
+ *   fa_fwd(variant=FA_VARIANT_OPT)     <- _flash_attn_fwd_kernel_optimize_shared_mem[...]   flash_atten.py:136-172
+ *   fa_fwd(variant=FA_VARIANT_SLICED)  <- _flash_attn_fwd_kernel_block_d_nomask_contiguous  flash_atten.py:261-275
+ *                                         (re-defined as split-KV partials + LSE merge)
+ *   gemm_f16                           <- _matmul_contiguous_kernel[grid](a,b,c,M,N,K,...)  mma.py:8-21
+ *   fa_device_limits                   <- get_sm_resource_limits()                         exceptions.py:760-775
+ *   fa_kernel_resources                <- Triton compile metadata (shared, n_regs)          tuner.py:341-376
+ */
+#ifndef FA_GFX950_H
+#define FA_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+enum {
+  FA_OK = 0,
+  FA_EINVAL = 1,      /* bad shape, stride, pointer or argument combination          */
+  FA_ENOTSUP = 2,     /* head dim / dtype / tile configuration not built              */
+  FA_EHIP = 3,        /* a HIP runtime call failed (message carries hipGetErrorString) */
+  FA_EWORKSPACE = 4,  /* split-KV workspace missing or too small                      */
+};
+
+enum { FA_DTYPE_F16 = 0, FA_DTYPE_BF16 = 1 };
+
+/* The three reference kernels (flash_atten.py:364-368). */
+enum { FA_VARIANT_BASIC = 0, FA_VARIANT_OPT = 1, FA_VARIANT_SLICED = 2 };
+
+/* One attention tile configuration. block_m = waves * rows_per_wave (rows_per_wave in {32, 64});
+ * block_n = KV rows per LDS tile; stages = K/V LDS buffers (1 single-buffered, 2 double-buffered);
+ * splits = KV splits of the sliced variant (1 = no split, no merge pass). */
+typedef struct {
+  int32_t block_m;
+  int32_t block_n;
+  int32_t waves;
+  int32_t stages;
+  int32_t splits;
+} fa_tile;
+
+/* Arguments of one attention forward. Tensors are [batch, heads, seq, head_dim] with element
+ * strides (the 16 stride arguments of flash_atten.py:20-39); the head_dim stride must be 1.
+ * H_kv divides H (grouped-query attention: query head h reads kv head h / (H / H_kv)).
+ * lse (nullable) is fp32 [B, H, M] with strides lse_stride: natural-log sum-exp of the scaled
+ * logits, as flash_atten.py:130-133. workspace is required when variant == SLICED and
+ * tile.splits > 1; its size is fa_fwd_workspace_bytes(). causal is top-left (row i sees keys
+ * j <= i), as flash_atten.py:103-105. */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t lse_stride[3];
+  int32_t B, H, H_kv, M, N, D;
+  float sm_scale;
+  int32_t dtype;
+  int32_t causal;
+  int32_t variant;
+  fa_tile tile;
+} fa_fwd_args;
+
+/* GEMM tile configuration: block_m x block_n macro tile, block_k deep, waves per workgroup,
+ * group_m rows of tiles per L2 group (mma.py:22-30 GROUP_M). */
+typedef struct {
+  int32_t block_m;
+  int32_t block_n;
+  int32_t block_k;
+  int32_t waves;
+  int32_t group_m;
+} gemm_tile;
+
+/* Per-kernel resources, read from this library's own gfx950 code object. */
+typedef struct {
+  int32_t vgprs;          /* architectural VGPRs per lane                  */
+  int32_t agprs;          /* accumulation VGPRs per lane (-1 if unknown)   */
+  int32_t sgprs;          /* scalar registers per wave (-1 if unknown)     */
+  int32_t lds_bytes;      /* static LDS per workgroup                      */
+  int32_t scratch_bytes;  /* private (spill) bytes per lane                */
+  int32_t threads;        /* threads per workgroup                         */
+  int32_t max_threads;    /* largest workgroup the kernel accepts          */
+} fa_resources;
+
+/* Device limits (the keys of exceptions.py:766-774, in gfx950 terms). */
+typedef struct {
+  int32_t lds_bytes_per_cu;
+  int32_t registers_per_simd;       /* 512 VGPR+AGPR lanes-registers x 64 lanes              */
+  int32_t register_file_bytes_per_simd;
+  int32_t wavefront_size;
+  int32_t max_threads_per_block;
+  int32_t cu_count;
+  int32_t clock_khz;
+  int32_t gcn_arch;                 /* e.g. 950                                              */
+} fa_device_limits_t;
+
+int fa_abi_version(void);
+
+/* Thread-local text of the last error returned on this thread ("" if none). */
+const char* fa_last_error(void);
+
+/* Attention forward; launches on `stream`. */
+int fa_fwd(const fa_fwd_args* args, void* stream);
+
+/* Bytes of split-KV workspace fa_fwd needs for these sizes (0 when splits <= 1). */
+int64_t fa_fwd_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t D, int32_t splits);
+
+/* Is this (variant, dtype, D, tile) built? Returns FA_OK or FA_ENOTSUP. */
+int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile);
+
+/* C[M,N] (fp16, row stride ldc) = A[M,K] (fp16, lda) x B[K,N] (fp16, ldb), fp32 accumulation;
+ * launches on `stream`. M, N, K must be multiples of the tile (mma.py:63-81 raises otherwise). */
+int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_t K,
+             int64_t lda, int64_t ldb, int64_t ldc, const gemm_tile* tile, void* stream);
+
+int gemm_f16_supported(const gemm_tile* tile);
+
+/* Resources of one built kernel: op 0 = attention (variant, dtype, D, tile), op 1 = GEMM
+ * (gtile). Needs a device (hipFuncGetAttributes). */
+int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
+                        const gemm_tile* gtile, fa_resources* out);
+
+int fa_device_limits(int32_t device, fa_device_limits_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_GFX950_H */

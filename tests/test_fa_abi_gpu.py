@@ -1,0 +1,119 @@
+"""GPU parity of the attention kernels, called directly through the C ABI (fa_fwd), against the
+oracle (exact double-precision attention) on identical seeded inputs.
+
+Tolerance (north star): max |O - O_oracle| <= 2e-2 for fp16, <= 3e-2 for bf16; LSE within 1e-3
+(absolute, natural log units).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import hip_lib
+import oracle
+from helpers import ATOL, make_qkv, max_abs, to_device
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16 = torch.float16, torch.bfloat16
+BASIC, OPT, SLICED = hip_lib.FA_VARIANT_BASIC, hip_lib.FA_VARIANT_OPT, hip_lib.FA_VARIANT_SLICED
+
+# (variant, block_m, block_n, waves, stages)
+TILES = {
+    "basic128": (BASIC, 128, 64, 4, 1),
+    "opt128": (OPT, 128, 64, 4, 2),
+    "opt256w4": (OPT, 256, 64, 4, 2),
+    "opt256w8": (OPT, 256, 64, 8, 2),
+}
+
+
+def run_fa(q, k, v, *, variant, tile, causal, scale=None, with_lse=True, dtype=F16, device="cuda:0", splits=1):
+    qd, kd, vd = (to_device(x, dtype, device) for x in (q, k, v))
+    B, H, M, D = qd.shape
+    o = torch.empty_like(qd)
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=device) if with_lse else None
+    scale = D ** -0.5 if scale is None else scale
+    var, bm, bn, waves, stages = tile
+    t = hip_lib.make_tile(bm, bn, waves, stages, splits)
+    ws = None
+    nbytes = hip_lib.workspace_bytes(B, H, M, D, splits)
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    hip_lib.fa_fwd(qd, kd, vd, o, lse, sm_scale=scale, causal=causal, variant=variant if variant is not None else var,
+                   tile=t, workspace=ws)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), (lse.cpu().numpy() if lse is not None else None)
+
+
+CASES = [
+    # name, B, H, Hkv, M, N, D, dtype, causal, tile
+    ("cfg1_d64", 1, 4, 4, 512, 512, 64, F16, False, "basic128"),
+    ("cfg1_d64_opt", 1, 4, 4, 512, 512, 64, F16, False, "opt128"),
+    ("d128_noncausal", 1, 2, 2, 512, 512, 128, F16, False, "opt128"),
+    ("d128_causal", 1, 2, 2, 512, 512, 128, F16, True, "opt128"),
+    ("d128_causal_basic", 1, 2, 2, 384, 384, 128, F16, True, "basic128"),
+    ("d128_w4r2", 2, 2, 2, 512, 512, 128, F16, False, "opt256w4"),
+    ("d128_w8", 2, 2, 2, 512, 512, 128, F16, True, "opt256w8"),
+    ("d256_bf16", 1, 2, 2, 256, 256, 256, BF16, False, "opt128"),
+    ("d256_f16_basic", 1, 2, 2, 256, 320, 256, F16, False, "basic128"),
+    ("gqa_6to1_causal", 1, 12, 2, 256, 256, 128, BF16, True, "opt128"),
+    ("ragged_m_n", 2, 3, 3, 200, 333, 64, F16, False, "opt128"),
+    ("ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "opt256w8"),
+    ("tiny", 1, 1, 1, 1, 1, 64, F16, False, "basic128"),
+    ("m_ne_n_causal", 1, 2, 2, 100, 260, 64, BF16, True, "opt128"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_fa_parity(gpu, case):
+    name, B, H, Hkv, M, N, D, dtype, causal, tile_name = case
+    print(f"[fa_abi] {name} B={B} H={H} Hkv={Hkv} M={M} N={N} D={D} {dtype} causal={causal} tile={tile_name}",
+          flush=True)
+    q, k, v = make_qkv(1000 + len(name), B, H, Hkv, M, N, D, dtype)
+    o, lse = run_fa(q, k, v, variant=None, tile=TILES[tile_name], causal=causal, dtype=dtype)
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
+    assert np.isfinite(o).all()
+    err = max_abs(o, o_ref)
+    assert err <= ATOL[dtype], f"max abs error {err}"
+    assert max_abs(lse, lse_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("splits", [2, 3, 8])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fa_sliced_split_kv(gpu, splits, causal):
+    B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, F16
+    print(f"[fa_abi] sliced splits={splits} causal={causal}", flush=True)
+    q, k, v = make_qkv(77, B, H, Hkv, M, N, D, dtype)
+    o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES["opt128"], causal=causal, dtype=dtype, splits=splits)
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
+    assert max_abs(o, o_ref) <= ATOL[dtype]
+    assert max_abs(lse, lse_ref) <= 1e-3
+
+
+def test_fa_matches_reference_online_algorithm(gpu):
+    """Against the reference kernel's own blocked algorithm (P rounded to fp16): tighter bound."""
+    B, H, M, N, D = 1, 2, 256, 256, 64
+    q, k, v = make_qkv(5, B, H, H, M, N, D, F16)
+    o, _ = run_fa(q, k, v, variant=None, tile=TILES["opt128"], causal=False)
+    o_ref, _ = oracle.attention_online(q, k, v, block_n=64, dtype=oracle.DTYPE_F16)
+    assert max_abs(o, o_ref) <= 4e-3
+
+
+def test_gemm_parity(gpu):
+    for (M, N, K, tile) in [(256, 256, 256, (256, 256, 64, 4, 8)), (512, 384, 320, (128, 128, 64, 4, 8)),
+                            (1024, 1024, 256, (128, 256, 64, 4, 8)), (512, 512, 512, (256, 256, 32, 4, 8))]:
+        print(f"[gemm_abi] M={M} N={N} K={K} tile={tile}", flush=True)
+        if M % tile[0] or N % tile[1] or K % tile[2]:
+            continue
+        a = oracle.round_to(oracle.portable_uniform(11, (M, K), -1, 1), 0)
+        b = oracle.round_to(oracle.portable_uniform(12, (K, N), -1, 1), 0)
+        ad = to_device(a, F16, "cuda:0")
+        bd = to_device(b, F16, "cuda:0")
+        cd = torch.empty((M, N), dtype=F16, device="cuda:0")
+        hip_lib.gemm_f16(ad, bd, cd, hip_lib.GemmTile(*tile))
+        torch.cuda.synchronize()
+        ref = oracle.gemm(a, b)
+        c = cd.float().cpu().numpy()
+        rel = float(np.linalg.norm(c - ref) / np.linalg.norm(ref))
+        assert rel <= 1e-3, rel
