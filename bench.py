@@ -1,0 +1,258 @@
+"""Headline benchmark: FlashAttention forward (fp16, B=4, H=32, N=8192, D=128, non-causal) and the
+fp16 GEMM at 8192^3 on one MI355X, through the drop-in API (tuner -> flash_attention, and
+_matmul_contiguous_kernel), i.e. the hand-written HIP kernels in libfa_gfx950.so.
+
+Prints ONE JSON line. `value` is the attention forward throughput in TFLOP/s (4*B*H*N^2*D per
+launch, test_flash_atten.py:234-240) with inputs resident in HBM; the GEMM figure (2*M*N*K,
+test_mma.py:78-83) is reported in the `gemm` object. Each launch is timed with HIP events recorded
+on the stream the kernels are launched on (torch's current stream), and the mean launch duration
+feeds `roofline.achieved`. The CPU baseline is the reference's own CPU path (torch SDPA math
+backend on fp32 CPU copies, test_flash_atten.py:459-461, 498-499; CPU torch.matmul, test_mma.py:
+260-261) on a bounded sample, extrapolated to the full workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--variant optimized]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "flash-attn-economical-gpu_amd"
+for _p in (str(PKG), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+PEAK_HBM_GBS = 8000.0
+SEED = 20260328  # the reference's constant (test_flash_atten.py:33)
+FA_SHAPE = dict(B=4, H=32, N=8192, D=128)
+GEMM_SHAPE = dict(M=8192, N=8192, K=8192)
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _time_launches(torch, fn, steps: int, warmup: int):
+    """Warm up, then time exactly `steps` launches; per-launch HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    outer_s, outer_e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    outer_s.record()
+    for s, e in events:
+        s.record()
+        fn()
+        e.record()
+    outer_e.record()
+    torch.cuda.synchronize()
+    per = [s.elapsed_time(e) for s, e in events]
+    return outer_s.elapsed_time(outer_e), per
+
+
+def _cpu_baseline_attention(torch, B, H, N, D, slices: int):
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    g = torch.Generator().manual_seed(SEED)
+    q, k, v = (torch.randn(1, 1, N, D, generator=g, dtype=torch.float16).float() for _ in range(3))
+    with sdpa_kernel(SDPBackend.MATH):
+        F.scaled_dot_product_attention(q, k, v)  # warm-up
+        times = []
+        for _ in range(slices):
+            t0 = time.perf_counter()
+            F.scaled_dot_product_attention(q, k, v)
+            times.append(time.perf_counter() - t0)
+    per_slice = statistics.mean(times)
+    full_s = per_slice * B * H
+    flops = 4.0 * B * H * N * N * D
+    return {
+        "value": flops / full_s / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (f"torch CPU SDPA math backend, fp32 copies of fp16 inputs, {slices} timed (b,h) slices of "
+                   f"[1,1,{N},{D}] after 1 warm-up, mean {per_slice * 1e3:.1f} ms/slice, extrapolated x{B * H} "
+                   f"to B={B} H={H} ({full_s:.1f} s); affinity cores={len(os.sched_getaffinity(0))}"),
+    }
+
+
+def _cpu_baseline_gemm(torch, M, N, K):
+    g = torch.Generator().manual_seed(SEED)
+    a = (torch.rand(M, K, generator=g) * 2 - 1).half()
+    b = (torch.rand(K, N, generator=g) * 2 - 1).half()
+    t0 = time.perf_counter()
+    torch.matmul(a, b)
+    dt = time.perf_counter() - t0
+    return {
+        "value": 2.0 * M * N * K / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": f"CPU torch.matmul fp16 {M}x{K} @ {K}x{N}, 1 run ({dt:.2f} s)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--variant", default="optimized", choices=["basic", "optimized", "sliced"])
+    ap.add_argument("--cpu-slices", type=int, default=4)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one MI355X only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the attention/GEMM path is single-GPU here: shard B*H (or KV splits) per GPU as DESIGN.md describes.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (gfx950)", file=sys.stderr)
+        return 1
+    import flash_atten
+    import hip_lib
+    import mma
+    import tuner
+
+    dev = torch.device("cuda:0")
+    limits = hip_lib.device_limits(0)
+    _log(f"device gfx{limits['gcn_arch']} CUs={limits['cu_count']} clock={limits['clock_khz'] / 1e6:.2f} GHz")
+
+    # ---- attention forward ----------------------------------------------------------------------
+    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
+    g = torch.Generator().manual_seed(SEED)
+    q, k, v = (torch.randn(B, H, N, D, generator=g, dtype=torch.float16).to(dev) for _ in range(3))
+    tuner_cls = {
+        "basic": tuner.FlashAttentionTuner,
+        "optimized": tuner.FlashAttentionOptimizeSharedMemTuner,
+        "sliced": tuner.FlashAttentionBlockDNomaskTuner,
+    }[args.variant]
+    spec = tuner_cls(tuple(q.shape), tuple(k.shape), tuple(v.shape), q.element_size(), causal=False,
+                     return_lse=False).build_flash_attention_launch_spec(q, k, v)
+    fa_flops = 4.0 * B * H * N * N * D
+    _log(f"attention {args.variant}: tile {spec.kernel_kwargs['BLOCK_M']}x{spec.kernel_kwargs['BLOCK_N']} "
+         f"waves={spec.kernel_kwargs['num_warps']} stages={spec.kernel_kwargs['num_stages']}")
+    total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup)
+    fa_launch_ms = statistics.mean(per)
+    fa_tflops_launch = fa_flops / (fa_launch_ms * 1e-3) / 1e12
+    fa_ms_per_step = total_ms / args.steps
+    fa_tflops = fa_flops / (fa_ms_per_step * 1e-3) / 1e12
+    _log(f"attention: {fa_ms_per_step:.3f} ms/step, {fa_tflops:.1f} TFLOP/s "
+         f"({100 * fa_tflops / PEAK_FP16_TFLOPS:.1f}% of dense fp16 peak)")
+
+    # parity spot check on 64 sampled rows against fp32 math on the GPU
+    o = spec.kernel_args[3]
+    rows = torch.randint(0, B * H * N, (64,), generator=torch.Generator().manual_seed(1))
+    bh, m = rows // N, rows % N
+    qs = q.reshape(B * H, N, D)[bh, m].float()
+    ks = k.reshape(B * H, N, D)[bh].float()
+    vs = v.reshape(B * H, N, D)[bh].float()
+    p = torch.softmax(torch.einsum("rd,rnd->rn", qs.to(dev), ks) * D ** -0.5, dim=-1)
+    ref = torch.einsum("rn,rnd->rd", p, vs)
+    fa_err = (o.reshape(B * H, N, D)[bh, m].float() - ref).abs().max().item()
+    del q, k, v, spec, o, qs, ks, vs, p, ref
+    torch.cuda.empty_cache()
+
+    # ---- GEMM ---------------------------------------------------------------------------------------
+    M, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
+    a = (torch.rand(M, K, generator=g) * 2 - 1).half().to(dev)
+    b = (torch.rand(K, Ng, generator=g) * 2 - 1).half().to(dev)
+    c = torch.empty(M, Ng, dtype=torch.float16, device=dev)
+    bm, bn, bk, group_m, warps, stages = mma._select_2d_contiguous_config(M, Ng, K)
+    grid = (math.ceil(M / bm) * math.ceil(Ng / bn),)
+
+    def gemm():
+        mma._matmul_contiguous_kernel[grid](a, b, c, M, Ng, K, BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=group_m,
+                                            USE_CACHE_EVICTION_HINTS=True, num_warps=warps, num_stages=stages)
+
+    g_total, g_per = _time_launches(torch, gemm, args.steps, args.warmup)
+    gemm_flops = 2.0 * M * Ng * K
+    gemm_launch_ms = statistics.mean(g_per)
+    gemm_tflops = gemm_flops / (g_total / args.steps * 1e-3) / 1e12
+    ref = a.float() @ b.float()
+    gemm_rel = ((c.float() - ref).norm() / ref.norm()).item()
+    _log(f"gemm {bm}x{bn}x{bk}: {g_total / args.steps:.3f} ms, {gemm_tflops:.1f} TFLOP/s, rel_fro={gemm_rel:.2e}")
+    del a, b, c, ref
+    torch.cuda.empty_cache()
+
+    # ---- CPU baseline (reference CPU path, bounded sample) ---------------------------------------
+    cpu_fa = cpu_gemm = None
+    if not args.no_cpu:
+        _log("timing the CPU baseline (bounded sample)")
+        cpu_fa = _cpu_baseline_attention(torch, B, H, N, D, args.cpu_slices)
+        cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K)
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if traffic_file.exists():
+        try:
+            traffic = json.loads(traffic_file.read_text()).get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    line = {
+        "metric": "FA fwd TFLOP/s + % fp16 MFMA peak (D=128,N=8k); GEMM TFLOP/s at 8192^3",
+        "value": round(fa_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(fa_ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (torch.randn fp16, seed 20260328)",
+        "config": {"workload": f"FlashAttention forward, {args.variant} variant, non-causal, sm_scale=1/sqrt(D)",
+                   "B": B, "H": H, "N": N, "D": D, "causal": False},
+        "mfma_peak_frac": round(fa_tflops / PEAK_FP16_TFLOPS, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(fa_tflops_launch, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(fa_tflops_launch / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel_ms": round(fa_launch_ms, 4),
+            "algorithmic_flop_per_launch": fa_flops,
+            "algorithmic_bytes_per_launch": 4 * B * H * N * D * 2,
+        },
+        "cpu_baseline": cpu_fa,
+        "parity": {"fa_max_abs_err_64_rows": fa_err, "gemm_rel_fro": gemm_rel},
+        "gemm": {
+            "metric": "GEMM fp16 TFLOP/s at 8192^3",
+            "value": round(gemm_tflops, 2),
+            "ms_per_step": round(g_total / args.steps, 4),
+            "tile": [bm, bn, bk, group_m],
+            "roofline": {
+                "bound": "mfma",
+                "achieved": round(gemm_flops / (gemm_launch_ms * 1e-3) / 1e12, 2),
+                "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(gemm_flops / (gemm_launch_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                "kernel_ms": round(gemm_launch_ms, 4),
+            },
+            "cpu_baseline": cpu_gemm,
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -403,6 +403,8 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 2, 1)
 
 #define FA_ENTRIES_D_WIDE(TAG, DTYPE, D)                    \
+  FA_ENTRY(TAG, DTYPE, D, 4, 2, 64, 1, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 1, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 2, 64, 2, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 2, 64, 2, 1),                  \
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 2, 0),                  \

@@ -27,10 +27,11 @@ struct GemmKernel {
   static constexpr int B_ELEMS = BN * BSTR;
   static constexpr int STAGE_ELEMS = A_ELEMS + B_ELEMS;
   static constexpr int A_CHUNKS = BM * BK / 8;  // 16-byte chunks of an A slab
-  static constexpr int A_ITERS = A_CHUNKS / THREADS;
+  static constexpr int A_ITERS = (A_CHUNKS + THREADS - 1) / THREADS;
   static constexpr int B_QUADS = BK * BN / 32;  // 4(k) x 8(n) blocks of a B slab
-  static constexpr int B_ITERS = B_QUADS / THREADS;
-  static_assert(A_CHUNKS % THREADS == 0 && B_QUADS % THREADS == 0, "slab must split evenly");
+  static constexpr int B_ITERS = (B_QUADS + THREADS - 1) / THREADS;
+  static constexpr bool A_EVEN = A_CHUNKS % THREADS == 0;
+  static constexpr bool B_EVEN = B_QUADS % THREADS == 0;
   static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile shape");
 
   struct Prefetch {
@@ -44,15 +45,17 @@ struct GemmKernel {
     for (int i = 0; i < A_ITERS; ++i) {
       const int id = tid + i * THREADS;
       const int row = id / (BK / 8), c8 = id % (BK / 8);
-      pf.a[i] = *reinterpret_cast<const u32x4*>(a + (int64_t)row * lda + k0 + c8 * 8);
+      if (A_EVEN || id < A_CHUNKS) pf.a[i] = *reinterpret_cast<const u32x4*>(a + (int64_t)row * lda + k0 + c8 * 8);
     }
 #pragma unroll
     for (int i = 0; i < B_ITERS; ++i) {
       const int id = tid + i * THREADS;
       const int kq = id / (BN / 8), n8 = id % (BN / 8);
+      if (B_EVEN || id < B_QUADS) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        pf.b[i][r] = *reinterpret_cast<const u32x4*>(b + (int64_t)(k0 + kq * 4 + r) * ldb + n8 * 8);
+        for (int r = 0; r < 4; ++r)
+          pf.b[i][r] = *reinterpret_cast<const u32x4*>(b + (int64_t)(k0 + kq * 4 + r) * ldb + n8 * 8);
+      }
     }
   }
 
@@ -61,12 +64,13 @@ struct GemmKernel {
     for (int i = 0; i < A_ITERS; ++i) {
       const int id = tid + i * THREADS;
       const int row = id / (BK / 8), c8 = id % (BK / 8);
-      *reinterpret_cast<u32x4*>(as + row * ASTR + c8 * 8) = pf.a[i];
+      if (A_EVEN || id < A_CHUNKS) *reinterpret_cast<u32x4*>(as + row * ASTR + c8 * 8) = pf.a[i];
     }
 #pragma unroll
     for (int i = 0; i < B_ITERS; ++i) {
       const int id = tid + i * THREADS;
       const int kq = id / (BN / 8), n8 = id % (BN / 8);
+      if (!(B_EVEN || id < B_QUADS)) continue;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int w = e >> 1;
@@ -169,6 +173,9 @@ static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(128, 128, 64, 2, 2),
     GEMM_ENTRY(128, 256, 64, 2, 2),
     GEMM_ENTRY(256, 128, 64, 2, 2),
+    GEMM_ENTRY(128, 128, 32, 2, 2),
+    GEMM_ENTRY(128, 64, 32, 2, 2),
+    GEMM_ENTRY(64, 256, 32, 2, 2),
 };
 
 const GemmKernelEntry* gemm_registry(int* count) {

@@ -1,0 +1,250 @@
+"""gfx950 launch-configuration search space, selection rules and the persisted tuning table.
+
+This replaces the reference's candidate enumeration and ranking (tuner.py:181-235, 414-449,
+503-517; mma.py:63-81). The reference compiles Triton candidates and ranks feasible ones by the
+largest resource footprint without timing. Here the candidates are the tiles built into
+libfa_gfx950.so; feasibility comes from the compiler's resource table (kernel_resources.json);
+ranking comes from a timed sweep on an MI355X (``tune_table.json``, written by gfx950_tune.py),
+with a fixed preference order when no measurement exists for a shape.
+
+Tune arguments given by a caller (FlashAttenTuneArguments, or the BLOCK_* kwargs of a kernel
+launch) are hints: a built tile that matches every given tile field is used; otherwise fields are
+relaxed in the order NUM_STAGES, NUM_WARPS, BLOCK_N, BLOCK_M and the relaxation is recorded.
+Tile choice never changes results, only speed.
+"""
+from __future__ import annotations
+
+import json
+import math
+from dataclasses import dataclass
+from pathlib import Path
+
+import hip_lib
+
+HERE = Path(__file__).resolve().parent
+TUNE_TABLE_PATH = HERE / "tune_table.json"
+
+VARIANT_BY_KERNEL = {
+    "_flash_attn_fwd_kernel_basic": hip_lib.FA_VARIANT_BASIC,
+    "_flash_attn_fwd_kernel_optimize_shared_mem": hip_lib.FA_VARIANT_OPT,
+    "_flash_attn_fwd_kernel_block_d_nomask_contiguous": hip_lib.FA_VARIANT_SLICED,
+}
+
+# Attention tiles in preference order (used when the tuning table has no entry for a shape):
+# (block_m, block_n, waves). stages follow the variant (basic 1, optimized/sliced 2).
+FA_TILE_SPACE = [
+    (256, 64, 8),
+    (256, 64, 4),
+    (128, 64, 4),
+    (256, 128, 8),
+    (128, 128, 4),
+    (256, 32, 8),
+    (128, 32, 4),
+]
+
+# GEMM tiles in preference order: (block_m, block_n, block_k, waves).
+GEMM_TILE_SPACE = [
+    (256, 256, 64, 4),
+    (256, 256, 32, 4),
+    (256, 128, 64, 4),
+    (128, 256, 64, 4),
+    (128, 128, 64, 4),
+    (128, 128, 32, 4),
+    (128, 64, 32, 4),
+    (64, 256, 32, 4),
+]
+GEMM_DEFAULT_GROUP_M = 8
+
+# Workgroups wanted in flight before the sliced variant stops splitting KV (2 per CU).
+TARGET_WORKGROUPS = 512
+MAX_SPLITS = 64
+
+
+@dataclass(frozen=True)
+class FaTileChoice:
+    block_m: int
+    block_n: int
+    waves: int
+    stages: int
+    splits: int = 1
+
+    def to_c(self) -> hip_lib.FaTile:
+        return hip_lib.make_tile(self.block_m, self.block_n, self.waves, self.stages, self.splits)
+
+
+def stages_for(variant: int) -> int:
+    return 1 if variant == hip_lib.FA_VARIANT_BASIC else 2
+
+
+def fa_candidates(variant: int, dtype, D: int) -> list[FaTileChoice]:
+    """Built attention tiles for (variant, dtype, D), in preference order."""
+    out = []
+    stages = stages_for(variant)
+    for bm, bn, waves in FA_TILE_SPACE:
+        choice = FaTileChoice(bm, bn, waves, stages, 1)
+        if hip_lib.fa_fwd_supported(variant, dtype, D, choice.to_c()):
+            out.append(choice)
+    return out
+
+
+def gemm_candidates() -> list[tuple[int, int, int, int]]:
+    return [t for t in GEMM_TILE_SPACE if hip_lib.gemm_supported(hip_lib.GemmTile(t[0], t[1], t[2], t[3], 1))]
+
+
+# ---- hint resolution ----------------------------------------------------------------------------
+
+_RELAX_ORDER = ("NUM_STAGES", "NUM_WARPS", "BLOCK_N", "BLOCK_M")
+
+
+def _matches(choice: FaTileChoice, hints: dict[str, int]) -> bool:
+    if "BLOCK_M" in hints and choice.block_m != hints["BLOCK_M"]:
+        return False
+    if "BLOCK_N" in hints and choice.block_n != hints["BLOCK_N"]:
+        return False
+    if "NUM_WARPS" in hints and choice.waves != hints["NUM_WARPS"]:
+        return False
+    if "NUM_STAGES" in hints and choice.stages != hints["NUM_STAGES"]:
+        return False
+    return True
+
+
+def filter_by_hints(candidates: list[FaTileChoice], hints: dict[str, int | None]) -> tuple[list[FaTileChoice], list[str]]:
+    """Candidates matching the given hints, relaxing hints in _RELAX_ORDER until some match.
+    Returns (matching candidates, names of relaxed hints)."""
+    active = {k: int(v) for k, v in hints.items() if v is not None and k in _RELAX_ORDER}
+    relaxed: list[str] = []
+    for key in _RELAX_ORDER:
+        if any(_matches(c, active) for c in candidates):
+            break
+        if key in active:
+            del active[key]
+            relaxed.append(key)
+    # Put back every dropped hint that some candidate still satisfies together with the rest.
+    for key in list(relaxed):
+        trial = dict(active)
+        trial[key] = int(hints[key])
+        if any(_matches(c, trial) for c in candidates):
+            active = trial
+            relaxed.remove(key)
+    found = [c for c in candidates if _matches(c, active)]
+    return (found or list(candidates)), relaxed
+
+
+# ---- tuning table -------------------------------------------------------------------------------
+
+_table_cache: dict | None = None
+
+
+def load_tune_table(path: Path | None = None) -> dict:
+    global _table_cache
+    if path is None and _table_cache is not None:
+        return _table_cache
+    p = path or TUNE_TABLE_PATH
+    table = json.loads(p.read_text()) if p.exists() else {"fa": {}, "gemm": {}}
+    table.setdefault("fa", {})
+    table.setdefault("gemm", {})
+    if path is None:
+        _table_cache = table
+    return table
+
+
+def reset_tune_table_cache() -> None:
+    global _table_cache
+    _table_cache = None
+
+
+def _bucket(x: int) -> int:
+    """Power-of-two bucket (>= 1) used to key shapes in the tuning table."""
+    return 1 << max(0, math.ceil(math.log2(max(1, x))))
+
+
+def fa_table_key(variant: int, dtype, D: int, causal: bool, B: int, H: int, M: int, N: int) -> str:
+    dt = "bf16" if "bfloat16" in str(dtype) else "f16"
+    return f"v{variant}|{dt}|D{D}|c{int(bool(causal))}|BH{_bucket(B * H)}|M{_bucket(M)}|N{_bucket(N)}"
+
+
+def gemm_table_key(M: int, N: int, K: int) -> str:
+    return f"M{_bucket(M)}|N{_bucket(N)}|K{_bucket(K)}"
+
+
+def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M: int, N: int,
+                   candidates: list[FaTileChoice]) -> FaTileChoice:
+    """Timed-table winner among candidates if recorded, else the first candidate (preference order)."""
+    entry = load_tune_table()["fa"].get(fa_table_key(variant, dtype, D, causal, B, H, M, N))
+    if entry is not None:
+        for c in candidates:
+            if (c.block_m, c.block_n, c.waves) == tuple(entry["tile"]):
+                return c
+    return candidates[0]
+
+
+def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int) -> int:
+    """KV splits for the sliced variant: split until ~TARGET_WORKGROUPS workgroups are in flight,
+    keeping at least two KV tiles per split."""
+    base = max(1, math.ceil(M / block_m) * B * H)
+    n_tiles = max(1, math.ceil(N / block_n))
+    if base >= TARGET_WORKGROUPS or n_tiles < 4:
+        return 1
+    splits = min(math.ceil(TARGET_WORKGROUPS / base), n_tiles // 2, MAX_SPLITS)
+    return max(1, splits)
+
+
+def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None = None) -> tuple[int, int, int, int, int]:
+    """(block_m, block_n, block_k, waves, group_m) for a GEMM; ValueError when no built tile divides.
+
+    Acceptance matches the reference selector (mma.py:63-81): K % 32 == 0 and either
+    (M % 128 == 0 and N % 64 == 0) or (M % 64 == 0 and N % 256 == 0)."""
+    if K % 32 != 0:
+        raise ValueError("fast 2D contiguous matmul requires K % 32 == 0")
+    cands = [t for t in gemm_candidates() if M % t[0] == 0 and N % t[1] == 0 and K % t[2] == 0]
+    if not cands:
+        raise ValueError(
+            "fast 2D contiguous matmul requires a supported divisible tile: "
+            "(M % 128 == 0 and N % 64 == 0), "
+            "(M % 128 == 0 and N % 128 == 0), or "
+            "(M % 64 == 0 and N % 256 == 0), with K % 32 == 0"
+        )
+    if hint is not None:
+        for t in cands:
+            if t[:3] == tuple(hint):
+                return (*t, _gemm_group_m(M, N, K, t))
+    entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
+    if entry is not None:
+        for t in cands:
+            if list(t) == list(entry["tile"]):
+                return (*t, int(entry.get("group_m", GEMM_DEFAULT_GROUP_M)))
+    t = cands[0]
+    return (*t, _gemm_group_m(M, N, K, t))
+
+
+def _gemm_group_m(M: int, N: int, K: int, tile) -> int:
+    entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
+    if entry is not None and list(entry["tile"]) == list(tile):
+        return int(entry.get("group_m", GEMM_DEFAULT_GROUP_M))
+    return GEMM_DEFAULT_GROUP_M
+
+
+# ---- compiled resources ---------------------------------------------------------------------------
+
+def fa_resources(variant: int, dtype, D: int, choice: FaTileChoice) -> dict[str, int] | None:
+    sym = hip_lib.fwd_kernel_symbol(variant, dtype, D, choice.to_c())
+    return _resources(sym)
+
+
+def gemm_resources(tile: tuple[int, int, int, int]) -> dict[str, int] | None:
+    sym = hip_lib.gemm_kernel_symbol(hip_lib.GemmTile(tile[0], tile[1], tile[2], tile[3], 1))
+    return _resources(sym)
+
+
+def _resources(sym: str) -> dict[str, int] | None:
+    raw = hip_lib.compiled_resources().get(sym)
+    if raw is None:
+        return None
+    return {
+        "vgprs": int(raw.get("VGPRs", 0)),
+        "agprs": int(raw.get("AGPRs", 0)),
+        "sgprs": int(raw.get("TotalSGPRs", 0)),
+        "lds_bytes": int(raw.get("LDS Size [bytes/block]", 0)),
+        "scratch_bytes_per_lane": int(raw.get("ScratchSize [bytes/lane]", 0)),
+        "waves_per_simd": int(raw.get("Occupancy [waves/SIMD]", 0)),
+    }

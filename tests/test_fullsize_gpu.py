@@ -1,0 +1,127 @@
+"""BASELINE.json configurations at full size (GPU): sampled rows against the oracle plus
+size-independent properties (first causal row copies V[0]; native GQA equals the expanded
+computation bit for bit; KV-split invariance; finite outputs), and the 8192^3 GEMM against an fp32
+product and sampled exact entries."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import hip_lib
+import mma
+import oracle
+from flash_atten import attention
+from helpers import ATOL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _randn(shape, seed, dtype, scale=1.0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=DEV, dtype=torch.float32) * scale).to(dtype)
+
+
+def _check_rows(q, k, v, out, causal, heads, rows_per_head=24, scale=None, tol=2e-2, seed=0):
+    """Oracle on `rows_per_head` random rows of each listed (b, h)."""
+    B, H, M, D = q.shape
+    Hkv = k.shape[1]
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for b, h in heads:
+        hk = h // (H // Hkv)
+        rows = np.sort(rng.choice(M, size=min(rows_per_head, M), replace=False))
+        rows[0] = 0
+        rows[-1] = M - 1
+        qs = q[b, h].float().cpu().numpy()[None, None]
+        ks = k[b, hk].float().cpu().numpy()[None, None]
+        vs = v[b, hk].float().cpu().numpy()[None, None]
+        o_ref, _ = oracle.attention_rows(qs, ks, vs, rows, causal=causal, scale=scale)
+        got = out[b, h].float().cpu().numpy()[rows]
+        worst = max(worst, float(np.abs(got - o_ref).max()))
+    assert worst <= tol, worst
+    return worst
+
+
+@pytest.mark.parametrize("variant", ["optimized", "basic", "sliced"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_headline_fa_fp16_b4h32n8192d128(gpu, variant, causal):
+    print(f"[fullsize] fa fp16 4x32x8192x128 causal={causal} {variant}", flush=True)
+    B, H, N, D = 4, 32, 8192, 128
+    q, k, v = (_randn((B, H, N, D), s, torch.float16) for s in (1, 2, 3))
+    out = attention(q, k, v, causal=causal, variant=variant)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_rows(q, k, v, out, causal, [(0, 0), (1, 17), (3, 31)], seed=int(causal))
+    if causal:
+        assert torch.equal(out[:, :, 0], v[:, :, 0])  # row 0 attends only key 0: O = V[0] exactly
+
+
+@pytest.mark.parametrize("N", [1024, 4096, 8192])
+def test_bf16_d256_b2h16_sliced(gpu, N):
+    """bf16, D=256, B=2, H=16, inputs N(0,1)*0.5, sliced split-KV + LSE merge."""
+    print(f"[fullsize] fa bf16 d256 N={N}", flush=True)
+    B, H, D = 2, 16, 256
+    q, k, v = (_randn((B, H, N, D), 10 + s, torch.bfloat16, 0.5) for s in range(3))
+    out, lse = attention(q, k, v, causal=False, variant="sliced", return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    _check_rows(q, k, v, out, False, [(0, 0), (1, 15)], tol=ATOL[torch.bfloat16])
+
+
+def test_split_invariance_and_lse(gpu):
+    """Sliced output is invariant (to fp16 output rounding) to the number of KV splits."""
+    B, H, M, N, D = 1, 8, 512, 8192, 128
+    q, k, v = (_randn((B, H, s_len, D), 20 + i, torch.float16) for i, s_len in enumerate((M, N, N)))
+    outs, lses = [], []
+    for splits in (1, 4, 16):
+        o = torch.empty_like(q)
+        lse = torch.empty((B, H, M), device=DEV, dtype=torch.float32)
+        ws_bytes = hip_lib.workspace_bytes(B, H, M, D, splits)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        hip_lib.fa_fwd(q, k, v, o, lse, sm_scale=D ** -0.5, causal=False, variant=hip_lib.FA_VARIANT_SLICED,
+                       tile=hip_lib.make_tile(256, 64, 8, 2, splits), workspace=ws if ws_bytes else None)
+        outs.append(o.float())
+        lses.append(lse)
+    torch.cuda.synchronize()
+    for o, lse in zip(outs[1:], lses[1:]):
+        assert (o - outs[0]).abs().max().item() <= 2e-3
+        assert (lse - lses[0]).abs().max().item() <= 1e-4
+
+
+def test_ttft_shape_gqa_bf16_causal(gpu):
+    """BASELINE configs[4] attention shape: [1,12,S,128] queries, 2 KV heads, bf16, causal."""
+    for S in (4096, 16384):
+        print(f"[fullsize] ttft-shape S={S}", flush=True)
+        q = _randn((1, 12, S, 128), 30, torch.bfloat16)
+        k = _randn((1, 2, S, 128), 31, torch.bfloat16)
+        v = _randn((1, 2, S, 128), 32, torch.bfloat16)
+        out = attention(q, k, v, causal=True, variant="sliced")
+        out_x = attention(q, k.repeat_interleave(6, dim=1), v.repeat_interleave(6, dim=1), causal=True,
+                          variant="sliced")
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_x)
+        _check_rows(q, k, v, out, True, [(0, 0), (0, 7), (0, 11)], tol=ATOL[torch.bfloat16])
+
+
+@pytest.mark.parametrize("n", [1024, 2048, 4096, 8192, 16384])
+def test_gemm_square_sweep(gpu, n):
+    """fp16 A,B ~ U[-1,1], fp32 accumulation; relative Frobenius <= 1e-3."""
+    print(f"[fullsize] gemm {n}^3", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(n)
+    a = (torch.rand((n, n), generator=g, device=DEV) * 2 - 1).half()
+    b = (torch.rand((n, n), generator=g, device=DEV) * 2 - 1).half()
+    c = mma.matmul(a, b)
+    ref = a.float() @ b.float()
+    torch.cuda.synchronize()
+    rel = ((c.float() - ref).norm() / ref.norm()).item()
+    assert rel <= 1e-3, rel
+    del ref
+    rng = np.random.default_rng(n)
+    ii, jj = rng.integers(0, n, 256), rng.integers(0, n, 256)
+    a_rows = a[torch.from_numpy(ii).to(DEV)].float().cpu().numpy()
+    b_cols = b[:, torch.from_numpy(jj).to(DEV)].float().cpu().numpy()
+    exact = np.einsum("tk,kt->t", a_rows.astype(np.float64), b_cols.astype(np.float64))
+    got = c[torch.from_numpy(ii).to(DEV), torch.from_numpy(jj).to(DEV)].float().cpu().numpy()
+    assert np.abs(got - exact).max() <= 2e-3 * np.sqrt(n / 1024) * 8 + np.abs(exact).max() * 2 ** -10
