@@ -59,46 +59,55 @@ def _time_launches(torch, fn, steps: int, warmup: int):
     return outer_s.elapsed_time(outer_e), per
 
 
-def _cpu_baseline_attention(torch, B, H, N, D, slices: int):
+def _cpu_baseline_attention(torch, B, H, N, D, slices: int, sample_n: int):
+    """torch CPU SDPA (math backend) on `slices` query blocks of `sample_n` rows of one (b, h) slice
+    against all N keys; the per-score time is extrapolated to B*H*N*N scores."""
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     g = torch.Generator().manual_seed(SEED)
-    q, k, v = (torch.randn(1, 1, N, D, generator=g, dtype=torch.float16).float() for _ in range(3))
+    q = torch.randn(1, 1, sample_n, D, generator=g, dtype=torch.float16).float()
+    k, v = (torch.randn(1, 1, N, D, generator=g, dtype=torch.float16).float() for _ in range(2))
     with sdpa_kernel(SDPBackend.MATH):
         F.scaled_dot_product_attention(q, k, v)  # warm-up
         times = []
-        for _ in range(slices):
+        for i in range(slices):
             t0 = time.perf_counter()
             F.scaled_dot_product_attention(q, k, v)
             times.append(time.perf_counter() - t0)
-    per_slice = statistics.mean(times)
-    full_s = per_slice * B * H
+            _log(f"cpu sdpa block {i + 1}/{slices}: {times[-1] * 1e3:.1f} ms")
+    per_block = statistics.mean(times)
+    full_s = per_block * (N / sample_n) * B * H
     flops = 4.0 * B * H * N * N * D
     return {
         "value": flops / full_s / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "reference",
-        "sample": (f"torch CPU SDPA math backend, fp32 copies of fp16 inputs, {slices} timed (b,h) slices of "
-                   f"[1,1,{N},{D}] after 1 warm-up, mean {per_slice * 1e3:.1f} ms/slice, extrapolated x{B * H} "
-                   f"to B={B} H={H} ({full_s:.1f} s); affinity cores={len(os.sched_getaffinity(0))}"),
+        "sample": (f"torch CPU SDPA math backend on fp32 copies of fp16 inputs (the reference's oracle path); "
+                   f"{slices} timed runs of a [1,1,{sample_n},{D}] query block against {N} keys after 1 warm-up, "
+                   f"mean {per_block * 1e3:.1f} ms, extrapolated x{(N // sample_n) * B * H} to B={B} H={H} "
+                   f"N={N} ({full_s:.1f} s); affinity cores={len(os.sched_getaffinity(0))}"),
     }
 
 
-def _cpu_baseline_gemm(torch, M, N, K):
+def _cpu_baseline_gemm(torch, M, N, K, sample: tuple[int, int, int]):
+    """CPU torch.matmul fp16 (the reference's CPU path) on a bounded sample shape, rate applied by FLOP."""
+    sm, sk, sn = sample
     g = torch.Generator().manual_seed(SEED)
-    a = (torch.rand(M, K, generator=g) * 2 - 1).half()
-    b = (torch.rand(K, N, generator=g) * 2 - 1).half()
+    a = (torch.rand(sm, sk, generator=g) * 2 - 1).half()
+    b = (torch.rand(sk, sn, generator=g) * 2 - 1).half()
     t0 = time.perf_counter()
     torch.matmul(a, b)
     dt = time.perf_counter() - t0
+    _log(f"cpu matmul {sm}x{sk}x{sn}: {dt * 1e3:.1f} ms")
     return {
-        "value": 2.0 * M * N * K / dt / 1e12,
+        "value": 2.0 * sm * sn * sk / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "reference",
-        "sample": f"CPU torch.matmul fp16 {M}x{K} @ {K}x{N}, 1 run ({dt:.2f} s)",
+        "sample": (f"CPU torch.matmul fp16 {sm}x{sk} @ {sk}x{sn} (test_mma.py's K=256), 1 run ({dt:.3f} s); "
+                   f"rate applied to {M}x{K}x{N}"),
     }
 
 
@@ -194,8 +203,8 @@ def main() -> int:
     cpu_fa = cpu_gemm = None
     if not args.no_cpu:
         _log("timing the CPU baseline (bounded sample)")
-        cpu_fa = _cpu_baseline_attention(torch, B, H, N, D, args.cpu_slices)
-        cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K)
+        cpu_fa = _cpu_baseline_attention(torch, B, H, N, D, args.cpu_slices, sample_n=512)
+        cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K, sample=(2048, 256, 2048))
 
     traffic = None
     traffic_file = ROOT / "profiles" / "traffic.json"
