@@ -77,6 +77,21 @@ __device__ inline float xhalf(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
+// max(x[l], x[l ^ 32]) in every lane with one v_permlane32_swap (a VALU op, no LDS round trip):
+// swapping lanes 32..63 of a copy with lanes 0..31 of another copy leaves, in each lane, its own
+// value in one result and its partner's value in the other.
+__device__ inline float xhalf_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float xhalf_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroup id remapped so that consecutive logical ids land on the same XCD. Workgroups are

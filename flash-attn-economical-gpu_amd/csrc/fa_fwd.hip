@@ -10,17 +10,24 @@
 //    keys per 32x32 tile, so the row max / sum / rescale factor are per-lane scalars and the only
 //    cross-lane step is one exchange between the two half-waves.
 //  * Q^T is the B operand and stays in VGPRs for the whole kernel (loaded once).
-//  * P^T is fed to the PV product O^T = V^T P^T directly from the S^T accumulator registers (the
-//    B-operand k-slots of a 16-key chunk are exactly the accumulator rows the lane already holds),
-//    so P never goes through LDS. V^T is the A operand, read from an LDS copy of V that is stored
-//    transposed ([d][key]) with keys permuted inside each 16-key chunk (bits 2 and 3 swapped) so
-//    that one 16-byte LDS read yields the 8 keys a lane needs.
-//  * K (natural [key][d]) and V^T tiles go through LDS; stages=1 single-buffers them (basic),
-//    stages=2 double-buffers them with one barrier per tile (optimized). Both prefetch the next
-//    tile from HBM into registers while the current tile is computed.
-//  * Softmax uses exp2 with scale*log2(e) folded into one FMA per score.
+//  * P^T is fed to O^T = V^T P^T directly from the S^T accumulator registers (the B-operand k-slots
+//    of a 16-key chunk are exactly 8 accumulator rows the lane already holds), so P never goes
+//    through LDS. V^T is the A operand, read from V stored naturally ([key][d]) in LDS with the
+//    gfx950 transposing read ds_read_b64_tr_b16: in a 16-lane group, result lane i element c is
+//    element (i & 3) of the 8-byte chunk addressed by group lane 4c + (i >> 2). Each lane of group
+//    lane L addresses key J + (L >> 2), columns d0 + 4 (L & 3); lane i then holds V[J + c][d0 + i].
+//  * K and V tiles are staged HBM -> registers -> LDS with precomputed per-thread addresses; the
+//    next tile's global loads are issued before the current tile is computed.
+//  * stages=1 (basic): one LDS buffer, two barriers per tile.
+//    stages=2 (optimized / sliced): K/V double-buffered in LDS, one barrier per tile.
+//    LDS fragment reads are issued a few MFMAs ahead of use (scheduling-group hints).
+//  * Softmax in the exp2 domain with scale*log2(e) folded into one FMA per score; the O rescale is
+//    lazy: the exponent offset only moves when a row max grows by more than 8 (log2 units), so
+//    P <= 256 and the 4*D accumulator multiplies run on a handful of tiles per row. The row sum is
+//    accumulated from the rounded P (v_dot2 with (1, 1)), i.e. the same P the PV product uses.
 //  * Causal (top-left, row i sees keys j <= i as flash_atten.py:103-105) skips KV tiles past the
-//    diagonal, masks only diagonal tiles, and walks query blocks heaviest-first.
+//    diagonal and waves whose rows all precede a tile, masks only diagonal tiles, and walks query
+//    blocks heaviest-first.
 //  * GQA: query head h reads KV head h / (H / H_kv); no K/V expansion.
 //  * Split-KV: the SPLIT instantiation writes fp32 normalised partial O and partial LSE per KV
 //    split; fa_merge_kernel combines them: lse = ln sum_j exp(lse_j), O = sum_j exp(lse_j - lse) O_j.
@@ -32,10 +39,28 @@ namespace fa {
 
 #define FA_NEG_INF (-__builtin_inff())
 
-// Position of key j (0 <= j < block_n) inside a V^T LDS row: bits 2 and 3 of j swapped, so that
-// the lane of half-wave `h` finds the 8 keys {16c + 4h + 0..3, 16c + 8 + 4h + 0..3} of chunk c
-// in one contiguous 16-byte run at slot 16c + 8h.
-__device__ inline int vt_slot(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// 4 x 16-bit transposing LDS read (see the header comment), returned as two dwords.
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+template <typename Tag>
+__device__ inline float dot2_sum(uint32_t packed, float acc);
+template <>
+__device__ inline float dot2_sum<f16_t>(uint32_t packed, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, packed), (h2){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+template <>
+__device__ inline float dot2_sum<bf16_t>(uint32_t packed, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, packed), (b2){(__bf16)1.0f, (__bf16)1.0f}, acc,
+                                         false);
+}
 
 template <typename Tag, int D, int WAVES, int RT, int BN, int STAGES, bool SPLIT>
 struct FwdKernel {
@@ -46,81 +71,178 @@ struct FwdKernel {
   static constexpr int DTL = D / 32;            // 32-row d tiles of O^T
   static constexpr int JT = BN / 32;            // 32-key tiles of S^T
   static constexpr int KC = BN / 16;            // 16-key chunks of P V
-  static constexpr int KSTR = D + 8;            // K LDS row stride (elements), +16 B pad
-  static constexpr int VSTR = BN + 8;           // V^T LDS row stride (elements), +16 B pad
+  static constexpr int KSTR = D + 8;            // K LDS row stride (elements): 16-byte skew
+  static constexpr int VSTR = D + 32;           // V LDS row stride (elements): 64-byte skew
   static constexpr int KTILE = BN * KSTR;
-  static constexpr int VTILE = D * VSTR;
-  static constexpr int STAGE_ELEMS = KTILE + VTILE;
-  static constexpr int K_CHUNKS = BN * D / 8;   // 16-byte chunks per K tile
-  static constexpr int K_ITERS = (K_CHUNKS + THREADS - 1) / THREADS;
-  static constexpr int V_QUADS = BN * D / 32;   // 4-key x 8-d blocks per V tile
-  static constexpr int V_ITERS = (V_QUADS + THREADS - 1) / THREADS;
+  static constexpr int VTILE = BN * VSTR;
+  static constexpr int CPR = D / 8;             // 16-byte chunks per K/V row
+  static constexpr int RSTEP = THREADS / CPR;   // rows covered by one pass of the workgroup
+  static constexpr int PASSES = (BN + RSTEP - 1) / RSTEP;
+  static constexpr float THRESH = 8.0f;         // lazy-rescale threshold (log2 units)
+  static constexpr bool kSumRounded = __is_same(Tag, f16_t);  // row sum from the rounded P
   static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+  static_assert(THREADS % CPR == 0, "threads must cover whole rows");
   static_assert(BM % BN == 0, "causal tile bound assumes block_m % block_n == 0");
 
   typedef DT<Tag> T;
+  typedef floatx16 STile[JT][RT];
 
-  struct Prefetch {
-    u32x4 k[K_ITERS];
-    u32x4 v[V_ITERS][4];
+  struct Ctx {
+    const uint16_t* kp;  // this thread's first K chunk (row r0, column c8) of tile 0
+    const uint16_t* vp;
+    int64_t sk2, sv2;    // row strides
+    int r0, c8;
+    int N;
   };
 
-  __device__ static inline void load_tile(Prefetch& pf, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t sk2, int64_t sv2, int n0, int N, int tid) {
+  __device__ static inline void load_rows(u32x4 (&dst)[PASSES], const uint16_t* base, int64_t stride, int n0,
+                                          const Ctx& cx) {
+    const uint16_t* p = base + (int64_t)n0 * stride;
+    const bool full = n0 + BN <= cx.N;
 #pragma unroll
-    for (int i = 0; i < K_ITERS; ++i) {
-      const int id = tid + i * THREADS;
-      const int row = id / (D / 8), c8 = id % (D / 8);
+    for (int i = 0; i < PASSES; ++i) {
+      const int row = cx.r0 + i * RSTEP;
       u32x4 val = {0u, 0u, 0u, 0u};
-      if ((K_CHUNKS % THREADS == 0 || id < K_CHUNKS) && n0 + row < N)
-        val = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(n0 + row) * sk2 + c8 * 8);
-      pf.k[i] = val;
+      if ((BN % RSTEP == 0 || row < BN) && (full || n0 + row < cx.N))
+        val = *reinterpret_cast<const u32x4*>(p + (int64_t)(i * RSTEP) * stride);
+      dst[i] = val;
     }
+  }
+
+  template <int STR>
+  __device__ static inline void store_rows(const u32x4 (&src)[PASSES], uint16_t* buf, const Ctx& cx) {
 #pragma unroll
-    for (int i = 0; i < V_ITERS; ++i) {
-      const int id = tid + i * THREADS;
-      const int jq = id / (D / 8), d8 = id % (D / 8);
+    for (int i = 0; i < PASSES; ++i) {
+      const int row = cx.r0 + i * RSTEP;
+      if (BN % RSTEP == 0 || row < BN) *reinterpret_cast<u32x4*>(buf + row * STR + cx.c8 * 8) = src[i];
+    }
+  }
+
+  // S^T tiles for one KV tile: s[jt][rt] = K[jt*32 + ., :] Q^T[:, rt*32 + .]
+  __device__ static inline void qk(STile& s, const u32x4 (&qf)[RT][DC], const uint16_t* ks, int lane_k_off) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = n0 + jq * 4 + r;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if ((V_QUADS % THREADS == 0 || id < V_QUADS) && j < N)
-          val = *reinterpret_cast<const u32x4*>(vbase + (int64_t)j * sv2 + d8 * 8);
-        pf.v[i][r] = val;
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[jt][rt][r] = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc) {
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + lane_k_off + jt * 32 * KSTR + cc * 16);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s[jt][rt] = T::mfma32(kf, qf[rt][cc], s[jt][rt]);
       }
     }
   }
 
-  __device__ static inline void store_tile(const Prefetch& pf, uint16_t* ks, uint16_t* vs, int tid) {
+  // Masks (only on tiles that need them), online softmax with lazy rescale, P packing. Leaves
+  // packed P in pk.
+  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][RT], floatx16 (&acc)[DTL][RT], float (&m_use)[RT],
+                                        float (&l_i)[RT], int n0, int wrow0, int col, int hh, const FwdParams& p) {
+    const float c = p.c;
+    const bool need_mask = (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
+    if (need_mask) {
 #pragma unroll
-    for (int i = 0; i < K_ITERS; ++i) {
-      const int id = tid + i * THREADS;
-      if (K_CHUNKS % THREADS == 0 || id < K_CHUNKS) {
-        const int row = id / (D / 8), c8 = id % (D / 8);
-        *reinterpret_cast<u32x4*>(ks + row * KSTR + c8 * 8) = pf.k[i];
-      }
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const int i = wrow0 + rt * 32 + col;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int j = n0 + jt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (j >= p.N || (p.causal && j > i)) s[jt][rt][r] = FA_NEG_INF;
+          }
+        }
     }
 #pragma unroll
-    for (int i = 0; i < V_ITERS; ++i) {
-      const int id = tid + i * THREADS;
-      if (V_QUADS % THREADS == 0 || id < V_QUADS) {
-        const int jq = id / (D / 8), d8 = id % (D / 8);
-        const int slot = vt_slot(jq * 4);
+    for (int rt = 0; rt < RT; ++rt) {
+      float mx = FA_NEG_INF;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int w = e >> 1;
-          const int sh = (e & 1) * 16;
-          const uint32_t a0 = (pf.v[i][0][w] >> sh) & 0xffffu, a1 = (pf.v[i][1][w] >> sh) & 0xffffu;
-          const uint32_t a2 = (pf.v[i][2][w] >> sh) & 0xffffu, a3 = (pf.v[i][3][w] >> sh) & 0xffffu;
-          u32x2 out = {a0 | (a1 << 16), a2 | (a3 << 16)};
-          *reinterpret_cast<u32x2*>(vs + (d8 * 8 + e) * VSTR + slot) = out;
-        }
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[jt][rt][r], s[jt][rt][r + 1]));
+      mx = xhalf_max(mx);
+      const bool need = mx > m_use[rt] + THRESH / c;
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float m_new = fmaxf(m_use[rt], mx);
+        const float alpha = (m_use[rt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[rt] - m_new) * c);
+        m_use[rt] = m_new;
+        l_i[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][rt][r] *= alpha;
+      }
+      const float mc = (m_use[rt] == FA_NEG_INF) ? 0.f : m_use[rt] * c;
+      float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int r = half * 8 + 2 * w;
+            const float e0 = fast_exp2(__builtin_fmaf(s[jt][rt][r], c, -mc));
+            const float e1 = fast_exp2(__builtin_fmaf(s[jt][rt][r + 1], c, -mc));
+            const uint32_t pw = T::pack2(e0, e1);
+            pk[jt * 2 + half][rt][w] = pw;
+            if (kSumRounded) {
+              // binary16 P (11-bit significand): summing the rounded pair moves l by <= 2^-12 relative
+              if (w & 1) l1 = dot2_sum<Tag>(pw, l1);
+              else l0 = dot2_sum<Tag>(pw, l0);
+            } else {
+              // bfloat16 P (8-bit significand) is too coarse for l: sum the fp32 values
+              if (w & 1) l1 += e0 + e1;
+              else l0 += e0 + e1;
+            }
+          }
+      l_i[rt] += l0 + l1;
+    }
+  }
+
+  // Scheduling hints (apply to the basic block they are emitted in): issue the LDS fragment reads
+  // a few MFMAs ahead of their use instead of waiting on each read right before its MFMA.
+  static constexpr int kReadAheadK = 4;  // K fragments (one ds_read_b128 each)
+  static constexpr int kReadAheadV = 2;  // V fragments (two ds_read_b64_tr_b16 each)
+  __device__ static inline void qk_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReadAheadK, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < DC * JT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+    }
+  }
+  __device__ static inline void pv_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kReadAheadV, 1);
+#pragma unroll
+    for (int i = 0; i < KC * DTL; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+  }
+
+  // O^T += V^T P^T
+  __device__ static inline void pv(floatx16 (&acc)[DTL][RT], const u32x4 (&pk)[KC][RT], const uint16_t* vs,
+                                   int lane_v_off) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) {
+        const uint16_t* base = vs + lane_v_off + kc * 16 * VSTR + dt * 32;
+        const u32x2 lo = lds_read_tr16(base);
+        const u32x2 hi = lds_read_tr16(base + 8 * VSTR);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = T::mfma32(vf, pk[kc][rt], acc[dt][rt]);
       }
     }
   }
 
   __device__ static void run(const FwdParams& p) {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[STAGES * STAGE_ELEMS];
+    constexpr int SMEM = (STAGES == 1) ? (KTILE + VTILE) : 2 * (KTILE + VTILE);
+    __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, col = lane & 31, hh = lane >> 5;
@@ -138,8 +260,14 @@ struct FwdKernel {
     const int wrow0 = m0 + wave * ROWS;  // first query row of this wave
 
     const uint16_t* qbase = p.q + (int64_t)b * p.sq0 + (int64_t)h * p.sq1;
-    const uint16_t* kbase = p.k + (int64_t)b * p.sk0 + (int64_t)hk * p.sk1;
-    const uint16_t* vbase = p.v + (int64_t)b * p.sv0 + (int64_t)hk * p.sv1;
+    Ctx cx;
+    cx.r0 = tid / CPR;
+    cx.c8 = tid % CPR;
+    cx.sk2 = p.sk2;
+    cx.sv2 = p.sv2;
+    cx.N = p.N;
+    cx.kp = p.k + (int64_t)b * p.sk0 + (int64_t)hk * p.sk1 + (int64_t)cx.r0 * p.sk2 + cx.c8 * 8;
+    cx.vp = p.v + (int64_t)b * p.sv0 + (int64_t)hk * p.sv1 + (int64_t)cx.r0 * p.sv2 + cx.c8 * 8;
 
     // Q^T fragments (B operand): lane holds row wrow0 + 32*rt + col, d = 16c + 8hh .. +7.
     u32x4 qf[RT][DC];
@@ -147,10 +275,10 @@ struct FwdKernel {
     for (int rt = 0; rt < RT; ++rt) {
       const int row = wrow0 + rt * 32 + col;
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
+      for (int cc = 0; cc < DC; ++cc) {
         u32x4 val = {0u, 0u, 0u, 0u};
-        if (row < p.M) val = *reinterpret_cast<const u32x4*>(qbase + (int64_t)row * p.sq2 + c * 16 + hh * 8);
-        qf[rt][c] = val;
+        if (row < p.M) val = *reinterpret_cast<const u32x4*>(qbase + (int64_t)row * p.sq2 + cc * 16 + hh * 8);
+        qf[rt][cc] = val;
       }
     }
 
@@ -160,12 +288,13 @@ struct FwdKernel {
     if (n_end > p.N) n_end = p.N;
     if (p.causal && n_end > m0 + BM) n_end = m0 + BM;
     const int t_end = (n_end + BN - 1) / BN;
+    const int ntiles = t_end > t_begin ? t_end - t_begin : 0;
 
     floatx16 acc[DTL][RT];
-    float m_i[RT], l_i[RT];
+    float m_use[RT], l_i[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      m_i[rt] = FA_NEG_INF;
+      m_use[rt] = FA_NEG_INF;
       l_i[rt] = 0.f;
 #pragma unroll
       for (int dt = 0; dt < DTL; ++dt)
@@ -173,127 +302,73 @@ struct FwdKernel {
         for (int r = 0; r < 16; ++r) acc[dt][rt][r] = 0.f;
     }
 
-    const float c = p.c;
-    Prefetch pf;
-    if (t_begin < t_end) {
-      load_tile(pf, kbase, vbase, p.sk2, p.sv2, t_begin * BN, p.N, tid);
-      if (STAGES == 2) {
-        store_tile(pf, smem, smem + KTILE, tid);
+    // Per-lane LDS fragment offsets.
+    const int lane_k_off = col * KSTR + hh * 8;
+    const int g = lane & 15;
+    const int lane_v_off = (4 * hh + (g >> 2)) * VSTR + 16 * ((lane >> 4) & 1) + 4 * (g & 3);
+
+    auto active = [&](int t) { return !(p.causal && t * BN > wrow0 + ROWS - 1); };
+
+    if (STAGES == 1) {
+      uint16_t* ks = smem;
+      uint16_t* vs = smem + KTILE;
+      u32x4 pkr[PASSES], pvr[PASSES];
+      if (ntiles > 0) {
+        load_rows(pkr, cx.kp, cx.sk2, t_begin * BN, cx);
+        load_rows(pvr, cx.vp, cx.sv2, t_begin * BN, cx);
+      }
+      for (int u = 0; u < ntiles; ++u) {
+        const int n0 = (t_begin + u) * BN;
+        __syncthreads();
+        store_rows<KSTR>(pkr, ks, cx);
+        store_rows<VSTR>(pvr, vs, cx);
+        __syncthreads();
+        if (u + 1 < ntiles) {
+          load_rows(pkr, cx.kp, cx.sk2, n0 + BN, cx);
+          load_rows(pvr, cx.vp, cx.sv2, n0 + BN, cx);
+        }
+        if (active(t_begin + u)) {
+          STile s;
+          u32x4 pk[KC][RT];
+          qk(s, qf, ks, lane_k_off);
+          qk_schedule();
+          softmax(s, pk, acc, m_use, l_i, n0, wrow0, col, hh, p);
+          pv(acc, pk, vs, lane_v_off);
+          pv_schedule();
+        }
+      }
+    } else {
+      // Double-buffered K/V tiles: tile u is computed from buffer u & 1 while tile u+1 travels
+      // HBM -> registers; the registers go to the other buffer after the compute, and one barrier
+      // per tile both publishes them and retires the buffer just read.
+      auto kb = [&](int i) { return smem + (i & 1) * (KTILE + VTILE); };
+      u32x4 pkr[PASSES], pvr[PASSES];
+      if (ntiles > 0) {
+        load_rows(pkr, cx.kp, cx.sk2, t_begin * BN, cx);
+        load_rows(pvr, cx.vp, cx.sv2, t_begin * BN, cx);
+        store_rows<KSTR>(pkr, kb(0), cx);
+        store_rows<VSTR>(pvr, kb(0) + KTILE, cx);
         __syncthreads();
       }
-    }
-
-    for (int t = t_begin; t < t_end; ++t) {
-      const int n0 = t * BN;
-      uint16_t* ks;
-      uint16_t* vs;
-      if (STAGES == 1) {
-        __syncthreads();  // every wave finished reading the previous tile
-        store_tile(pf, smem, smem + KTILE, tid);
-        __syncthreads();
-        ks = smem;
-        vs = smem + KTILE;
-        if (t + 1 < t_end) load_tile(pf, kbase, vbase, p.sk2, p.sv2, n0 + BN, p.N, tid);
-      } else {
-        const int cur = (t - t_begin) & 1;
-        ks = smem + cur * STAGE_ELEMS;
-        vs = ks + KTILE;
-        if (t + 1 < t_end) load_tile(pf, kbase, vbase, p.sk2, p.sv2, n0 + BN, p.N, tid);
-      }
-
-      // A wave whose rows all precede this tile (causal) has nothing to add from it.
-      const bool wave_active = !(p.causal && n0 > wrow0 + ROWS - 1);
-      if (wave_active) {
-        // S^T = K Q^T for JT x RT 32x32 tiles.
-        floatx16 s[JT][RT];
-#pragma unroll
-        for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[jt][rt][r] = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < DC; ++cc) {
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt) {
-            const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + (jt * 32 + col) * KSTR + cc * 16 + hh * 8);
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) s[jt][rt] = T::mfma32(kf, qf[rt][cc], s[jt][rt]);
-          }
+      for (int u = 0; u < ntiles; ++u) {
+        const int t = t_begin + u;
+        const int n0 = t * BN;
+        if (u + 1 < ntiles) {
+          load_rows(pkr, cx.kp, cx.sk2, n0 + BN, cx);
+          load_rows(pvr, cx.vp, cx.sv2, n0 + BN, cx);
         }
-
-        // Key-range and causal masks, only on tiles that need them.
-        const bool need_mask = (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
-        if (need_mask) {
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-              const int i = wrow0 + rt * 32 + col;
-#pragma unroll
-              for (int r = 0; r < 16; ++r) {
-                const int j = n0 + jt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                if (j >= p.N || (p.causal && j > i)) s[jt][rt][r] = FA_NEG_INF;
-              }
-            }
+        if (active(t)) {
+          STile s;
+          u32x4 pk[KC][RT];
+          qk(s, qf, kb(u), lane_k_off);
+          qk_schedule();
+          softmax(s, pk, acc, m_use, l_i, n0, wrow0, col, hh, p);
+          pv(acc, pk, kb(u) + KTILE, lane_v_off);
+          pv_schedule();
         }
-
-        // Online softmax (per-lane row statistics).
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          float mx = FA_NEG_INF;
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jt][rt][r]);
-          mx = fmaxf(mx, xhalf(mx));
-          const float m_new = fmaxf(m_i[rt], mx);
-          const float m_use = (m_new == FA_NEG_INF) ? 0.f : m_new;
-          const float alpha = fast_exp2((m_i[rt] - m_use) * c);
-          m_i[rt] = m_new;
-          const float mc = m_use * c;
-          float rs = 0.f;
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float e = fast_exp2(__builtin_fmaf(s[jt][rt][r], c, -mc));
-              s[jt][rt][r] = e;
-              rs += e;
-            }
-          l_i[rt] = l_i[rt] * alpha + rs;
-#pragma unroll
-          for (int dt = 0; dt < DTL; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[dt][rt][r] *= alpha;
-        }
-
-        // O^T += V^T P^T.
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          const int jt = kc >> 1, rb = (kc & 1) * 8;
-          u32x4 pb[RT];
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            pb[rt][0] = T::pack2(s[jt][rt][rb + 0], s[jt][rt][rb + 1]);
-            pb[rt][1] = T::pack2(s[jt][rt][rb + 2], s[jt][rt][rb + 3]);
-            pb[rt][2] = T::pack2(s[jt][rt][rb + 4], s[jt][rt][rb + 5]);
-            pb[rt][3] = T::pack2(s[jt][rt][rb + 6], s[jt][rt][rb + 7]);
-          }
-#pragma unroll
-          for (int dt = 0; dt < DTL; ++dt) {
-            const u32x4 vf = *reinterpret_cast<const u32x4*>(vs + (dt * 32 + col) * VSTR + kc * 16 + hh * 8);
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = T::mfma32(vf, pb[rt], acc[dt][rt]);
-          }
-        }
-      }
-
-      if (STAGES == 2) {
-        if (t + 1 < t_end) {
-          const int nxt = (t + 1 - t_begin) & 1;
-          uint16_t* kn = smem + nxt * STAGE_ELEMS;
-          store_tile(pf, kn, kn + KTILE, tid);
+        if (u + 1 < ntiles) {
+          store_rows<KSTR>(pkr, kb(u + 1), cx);
+          store_rows<VSTR>(pvr, kb(u + 1) + KTILE, cx);
         }
         __syncthreads();
       }
@@ -303,20 +378,20 @@ struct FwdKernel {
     constexpr float kLn2 = 0.69314718055994530942f;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float l = l_i[rt] + xhalf(l_i[rt]);
+      const float l = xhalf_sum(l_i[rt]);
       const int i = wrow0 + rt * 32 + col;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
-      const float lse_val = (l > 0.f) ? (m_i[rt] * c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      const float lse_val = (l > 0.f) ? (m_use[rt] * p.c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
       if (i < p.M) {
         if (SPLIT) {
           float* wo = p.ws_o + ((int64_t)(split * p.B * p.H + bh) * p.M + i) * D;
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              floatx4 val = {acc[dt][rt][4 * g] * inv, acc[dt][rt][4 * g + 1] * inv,
-                             acc[dt][rt][4 * g + 2] * inv, acc[dt][rt][4 * g + 3] * inv};
-              *reinterpret_cast<floatx4*>(wo + dt * 32 + 8 * g + 4 * hh) = val;
+            for (int gq = 0; gq < 4; ++gq) {
+              floatx4 val = {acc[dt][rt][4 * gq] * inv, acc[dt][rt][4 * gq + 1] * inv,
+                             acc[dt][rt][4 * gq + 2] * inv, acc[dt][rt][4 * gq + 3] * inv};
+              *reinterpret_cast<floatx4*>(wo + dt * 32 + 8 * gq + 4 * hh) = val;
             }
           if (hh == 0) p.ws_lse[(int64_t)(split * p.B * p.H + bh) * p.M + i] = lse_val;
         } else {
@@ -324,10 +399,10 @@ struct FwdKernel {
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              u32x2 val = {T::pack2(acc[dt][rt][4 * g] * inv, acc[dt][rt][4 * g + 1] * inv),
-                           T::pack2(acc[dt][rt][4 * g + 2] * inv, acc[dt][rt][4 * g + 3] * inv)};
-              *reinterpret_cast<u32x2*>(orow + dt * 32 + 8 * g + 4 * hh) = val;
+            for (int gq = 0; gq < 4; ++gq) {
+              u32x2 val = {T::pack2(acc[dt][rt][4 * gq] * inv, acc[dt][rt][4 * gq + 1] * inv),
+                           T::pack2(acc[dt][rt][4 * gq + 2] * inv, acc[dt][rt][4 * gq + 3] * inv)};
+              *reinterpret_cast<u32x2*>(orow + dt * 32 + 8 * gq + 4 * hh) = val;
             }
           if (p.lse != nullptr && hh == 0)
             p.lse[(int64_t)b * p.sl0 + (int64_t)h * p.sl1 + (int64_t)i * p.sl2] = lse_val;
@@ -408,7 +483,10 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 4, 2, 64, 2, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 2, 64, 2, 1),                  \
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 2, 0),                  \
-  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 2, 1)
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 2, 1),                  \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 1, 0),                 \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 128, 1, 0),                 \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 0)
 
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),
