@@ -45,9 +45,10 @@ FA_TILE_SPACE = [
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).
 GEMM_TILE_SPACE = [
     (256, 256, 64, 4),
-    (256, 256, 32, 4),
-    (256, 128, 64, 4),
-    (128, 256, 64, 4),
+    (256, 256, 64, 8),
+    (256, 256, 32, 8),
+    (256, 128, 64, 8),
+    (128, 256, 64, 8),
     (128, 128, 64, 4),
     (128, 128, 32, 4),
     (128, 64, 32, 4),

@@ -329,7 +329,7 @@ def fwd_kernel_symbol(variant: int, dtype: torch.dtype, D: int, tile: FaTile) ->
 
 
 def gemm_kernel_symbol(tile: GemmTile) -> str:
-    wm = 2 if tile.waves == 4 else (2 if tile.waves == 8 else 1)
+    wm = 2  # every built GEMM tile splits its waves 2 x (waves / 2)
     wn = tile.waves // wm
     return (
         f"_ZN2fa15gemm_f16_kernelILi{tile.block_m}ELi{tile.block_n}ELi{tile.block_k}ELi{wm}ELi{wn}EEEvNS_10GemmParamsE"

@@ -102,7 +102,9 @@ def test_fa_matches_reference_online_algorithm(gpu):
 
 def test_gemm_parity(gpu):
     for (M, N, K, tile) in [(256, 256, 256, (256, 256, 64, 4, 8)), (512, 384, 320, (128, 128, 64, 4, 8)),
-                            (1024, 1024, 256, (128, 256, 64, 4, 8)), (512, 512, 512, (256, 256, 32, 4, 8))]:
+                            (1024, 1024, 256, (128, 256, 64, 8, 8)), (512, 512, 512, (256, 256, 32, 8, 8)),
+                            (768, 512, 640, (256, 256, 64, 8, 3)), (256, 192, 96, (128, 64, 32, 4, 2)),
+                            (128, 512, 64, (64, 256, 32, 4, 1))]:
         print(f"[gemm_abi] M={M} N={N} K={K} tile={tile}", flush=True)
         if M % tile[0] or N % tile[1] or K % tile[2]:
             continue
