@@ -31,6 +31,8 @@ for _p in (str(PKG), str(ROOT)):
 
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on `--traffic-probe`.
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_fa_b4h32n8192d128_gemm8192.json"
 SEED = 20260328  # the reference's constant (test_flash_atten.py:33)
 FA_SHAPE = dict(B=4, H=32, N=8192, D=128)
 GEMM_SHAPE = dict(M=8192, N=8192, K=8192)
@@ -111,6 +113,30 @@ def _cpu_baseline_gemm(torch, M, N, K, sample: tuple[int, int, int]):
     }
 
 
+def _traffic_probe(torch, flash_atten, tuner, mma, dev) -> int:
+    """One dispatch each of: a 256 MiB fp32 copy (known bytes, calibrates the counters), the headline
+    attention forward, and the 8192^3 GEMM."""
+    g = torch.Generator().manual_seed(SEED)
+    src = torch.randn(64 * 1024 * 1024, generator=g).to(dev)
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+    del src
+    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
+    q, k, v = (torch.randn(B, H, N, D, generator=g, dtype=torch.float16).to(dev) for _ in range(3))
+    spec = tuner.FlashAttentionOptimizeSharedMemTuner(tuple(q.shape), tuple(k.shape), tuple(v.shape), 2, causal=False,
+                                                      return_lse=False).build_flash_attention_launch_spec(q, k, v)
+    flash_atten.flash_attention(spec)
+    torch.cuda.synchronize()
+    del q, k, v, spec
+    M, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
+    a = (torch.rand(M, K, generator=g) * 2 - 1).half().to(dev)
+    b = (torch.rand(K, Ng, generator=g) * 2 - 1).half().to(dev)
+    mma.matmul(a, b)
+    torch.cuda.synchronize()
+    _log("traffic probe done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +145,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--variant", default="optimized", choices=["basic", "optimized", "sliced"])
     ap.add_argument("--cpu-slices", type=int, default=4)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run one 256 MiB copy (counter calibration), one attention forward and one GEMM, then exit "
+                         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -139,6 +168,8 @@ def main() -> int:
     import tuner
 
     dev = torch.device("cuda:0")
+    if args.traffic_probe:
+        return _traffic_probe(torch, flash_atten, tuner, mma, dev)
     limits = hip_lib.device_limits(0)
     _log(f"device gfx{limits['gcn_arch']} CUs={limits['cu_count']} clock={limits['clock_khz'] / 1e6:.2f} GHz")
 
@@ -206,13 +237,14 @@ def main() -> int:
         cpu_fa = _cpu_baseline_attention(torch, B, H, N, D, args.cpu_slices, sample_n=512)
         cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K, sample=(2048, 256, 2048))
 
-    traffic = None
-    traffic_file = ROOT / "profiles" / "traffic.json"
-    if traffic_file.exists():
+    traffic = gemm_traffic = None
+    if TRAFFIC_FILE.exists():
         try:
-            traffic = json.loads(traffic_file.read_text()).get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
+            recorded = json.loads(TRAFFIC_FILE.read_text())
+            traffic = recorded.get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
+            gemm_traffic = recorded.get("gemm_f16_8192cube", {}).get("bytes_per_launch")
         except (ValueError, OSError):
-            traffic = None
+            traffic = gemm_traffic = None
 
     line = {
         "metric": "FA fwd TFLOP/s + % fp16 MFMA peak (D=128,N=8k); GEMM TFLOP/s at 8192^3",
@@ -254,7 +286,10 @@ def main() -> int:
                 "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(gemm_flops / (gemm_launch_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                "traffic": gemm_traffic,
                 "kernel_ms": round(gemm_launch_ms, 4),
+                "algorithmic_flop_per_launch": gemm_flops,
+                "algorithmic_bytes_per_launch": 2 * (M * K + K * Ng + M * Ng),
             },
             "cpu_baseline": cpu_gemm,
         },

@@ -413,7 +413,10 @@ struct FwdKernel {
 };
 
 template <typename Tag, int D, int WAVES, int RT, int BN, int STAGES, bool SPLIT>
-__global__ __launch_bounds__(WAVES * 64) void fa_fwd_kernel(FwdParams p) {
+// Four-wave workgroups with RT=1 and D <= 128 fit in 256 registers per lane, so two independent
+// workgroups share a CU (two waves per SIMD); their barriers only align four waves each.
+__global__ __launch_bounds__(WAVES * 64, (WAVES == 4 && RT == 1 && D <= 128) ? 2 : 1) void fa_fwd_kernel(
+    FwdParams p) {
   FwdKernel<Tag, D, WAVES, RT, BN, STAGES, SPLIT>::run(p);
 }
 
