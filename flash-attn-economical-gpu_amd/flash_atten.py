@@ -186,6 +186,37 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
     return out
 
 
+def sdpa(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, is_causal: bool = False,
+         scale: float | None = None, variant: str = "sliced") -> torch.Tensor:
+    """scaled_dot_product_attention-shaped entry for model code (no mask, no dropout).
+
+    q [B, H, M, D] and k/v [B, H_kv, N, D] are read through their strides (any batch/head/row
+    strides with a unit head-dim stride, e.g. the transposed projection views a decoder layer
+    passes), so no contiguous copies are made. H_kv may divide H (GQA). The result is a [B, H, M, D]
+    view of memory laid out [B, M, H, D], which is what a decoder's following
+    `.transpose(1, 2).contiguous()` wants (that copy becomes a no-op)."""
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise ValueError("sdpa expects 4-D [batch, heads, seq, head_dim] tensors")
+    B, H, M, D = query.shape
+    variant_code = {"basic": hip_lib.FA_VARIANT_BASIC, "optimized": hip_lib.FA_VARIANT_OPT,
+                    "sliced": hip_lib.FA_VARIANT_SLICED}[variant]
+    sm_scale = D ** -0.5 if scale is None else float(scale)
+    out = torch.empty((B, M, H, D), device=query.device, dtype=query.dtype).transpose(1, 2)
+    N = key.shape[2]
+    tile = _tile_for(variant_code, query.dtype, D, bool(is_causal), B, H, M, N, {})
+    splits = 1
+    workspace = None
+    if variant_code == hip_lib.FA_VARIANT_SLICED:
+        splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n)
+        need = hip_lib.workspace_bytes(B, H, M, D, splits)
+        if need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+    choice = cfgs.FaTileChoice(tile.block_m, tile.block_n, tile.waves, tile.stages, splits)
+    hip_lib.fa_fwd(query, key, value, out, None, sm_scale=sm_scale, causal=bool(is_causal), variant=variant_code,
+                   tile=choice.to_c(), workspace=workspace)
+    return out
+
+
 __all__ = [
     "flash_attention_kernel_mapping",
     "flash_attention",

@@ -1,0 +1,210 @@
+"""Time-to-first-token harness: prefill of a random-init Qwen2.5-1.5B-architecture decoder with every
+attention call routed through the gfx950 FlashAttention kernel.
+
+Modelled on the reference's TTFT benchmark (paths relative to the reference repository):
+  * SDPA replacement while the model runs (ttft.py:299-327): rejects dropout and explicit masks,
+    counts calls. Unlike the reference it honours `is_causal` (the reference forces non-causal,
+    ttft.py:251-262, 317-321) and passes grouped K/V heads natively (no repeat_interleave,
+    ttft.py:203-215); bf16 and fp16 are accepted (the reference accepts fp16 only, ttft.py:172-173).
+  * Prefill call: model(input_ids, use_cache=True, logits_to_keep=1) (ttft.py:401-408).
+  * Verification: final-token logits against torch's own scaled_dot_product_attention,
+    allclose(rtol=atol=0.1) plus argmax agreement (ttft.py:415-446).
+  * Timing: CUDA-event-timed prefills after warm-up (ttft.py:449-480).
+The model is built locally from the architecture numbers (28 layers, hidden 1536, 12 query / 2 KV
+heads of dim 128, SwiGLU 8960, RoPE base 1e6, RMSNorm, vocab 151936) with seeded random weights:
+there is no hub access. The prompt is seeded uniform-random token ids.
+
+Usage: python ttft_qwen.py --prompt-lens 4096 16384 [--layers 28] [--json out.json]
+"""
+from __future__ import annotations
+
+import argparse
+import contextlib
+import json
+import statistics
+import sys
+from dataclasses import dataclass
+from typing import Iterator
+
+import torch
+import torch.nn.functional as F
+
+import flash_atten
+
+QWEN25_1P5B = dict(
+    vocab_size=151936,
+    hidden_size=1536,
+    intermediate_size=8960,
+    num_hidden_layers=28,
+    num_attention_heads=12,
+    num_key_value_heads=2,
+    max_position_embeddings=32768,
+    rope_theta=1000000.0,
+    rms_norm_eps=1e-6,
+    tie_word_embeddings=True,
+    hidden_act="silu",
+)
+
+
+@dataclass
+class BackendUseStats:
+    calls: int = 0
+
+
+def build_model(*, seed: int = 0, layers: int | None = None, dtype: torch.dtype = torch.bfloat16,
+                device: str = "cuda", overrides: dict | None = None):
+    """Random-init Qwen2 decoder with the Qwen2.5-1.5B architecture (seeded)."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    arch = dict(QWEN25_1P5B)
+    if layers is not None:
+        arch["num_hidden_layers"] = int(layers)
+    arch.update(overrides or {})
+    config = Qwen2Config(**arch, attn_implementation="sdpa")
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = Qwen2ForCausalLM(config)
+    return model.to(dtype).eval()
+
+
+def make_prompt(prompt_len: int, vocab_size: int, *, seed: int = 0, device: str = "cuda") -> torch.Tensor:
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randint(0, vocab_size, (1, prompt_len), generator=g).to(device)
+
+
+def _unsupported(reason: str):
+    raise RuntimeError(f"gfx950 SDPA replacement: unsupported call ({reason})")
+
+
+@contextlib.contextmanager
+def patched_sdpa_with_gfx950(*, allow_causal: bool = True, stats: BackendUseStats | None = None,
+                             variant: str = "sliced") -> Iterator[None]:
+    """Replace F.scaled_dot_product_attention with the gfx950 kernel for the duration."""
+    original = F.scaled_dot_product_attention
+
+    def replacement(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
+                    enable_gqa=False):
+        if dropout_p != 0.0:
+            _unsupported(f"dropout_p={dropout_p}")
+        if attn_mask is not None:
+            _unsupported("attn_mask is not None")
+        if is_causal and not allow_causal:
+            _unsupported("is_causal=True")
+        if query.device.type != "cuda":
+            _unsupported(f"tensors on {query.device}")
+        if query.shape[1] != key.shape[1] and not enable_gqa:
+            _unsupported("head counts differ but enable_gqa=False")
+        if stats is not None:
+            stats.calls += 1
+        return flash_atten.sdpa(query, key, value, is_causal=is_causal, scale=scale, variant=variant)
+
+    F.scaled_dot_product_attention = replacement
+    try:
+        yield
+    finally:
+        F.scaled_dot_product_attention = original
+
+
+def prefill_logits(model, input_ids: torch.Tensor) -> torch.Tensor:
+    with torch.no_grad():
+        out = model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
+    return out.logits[:, -1, :]
+
+
+def time_ttft_ms(model, input_ids: torch.Tensor, *, warmup: int = 2, iters: int = 5) -> dict[str, float]:
+    for _ in range(warmup):
+        prefill_logits(model, input_ids)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        prefill_logits(model, input_ids)
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    return {"mean_ms": statistics.mean(times), "p50_ms": statistics.median(times), "min_ms": min(times)}
+
+
+def verify_against_torch(model, input_ids: torch.Tensor, *, variant: str = "sliced") -> dict[str, object]:
+    """Final-token logits with the gfx950 kernel vs torch's own SDPA (rtol=atol=0.1, argmax).
+
+    Also reports the noise floor: the same comparison between torch's default SDPA backend and its
+    math backend. Low-precision activations through many layers make two correct attention
+    implementations disagree by that much; `within_noise_floor` asks that ours stays within twice
+    the torch-vs-torch difference (or the 0.1 tolerance, whichever is larger)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    reference = prefill_logits(model, input_ids).float()
+    with sdpa_kernel(SDPBackend.MATH):
+        reference_math = prefill_logits(model, input_ids).float()
+    stats = BackendUseStats()
+    with patched_sdpa_with_gfx950(stats=stats, variant=variant):
+        ours = prefill_logits(model, input_ids).float()
+    diff = (ours - reference).abs()
+    floor = float((reference_math - reference).abs().max())
+    return {
+        "allclose_rtol_atol_0p1": bool(torch.allclose(ours, reference, rtol=0.1, atol=0.1)),
+        "argmax_match": bool(torch.equal(ours.argmax(-1), reference.argmax(-1))),
+        "max_abs_diff": float(diff.max()),
+        "mean_abs_diff": float(diff.mean()),
+        "max_abs_diff_vs_math_backend": float((ours - reference_math).abs().max()),
+        "noise_floor_torch_default_vs_math": floor,
+        "within_noise_floor": float(diff.max()) <= max(2.0 * floor, 0.1),
+        "logit_abs_max": float(reference.abs().max()),
+        "kernel_calls": stats.calls,
+    }
+
+
+def run(prompt_lens: list[int], *, layers: int | None = None, seed: int = 0, variant: str = "sliced",
+        warmup: int = 2, iters: int = 5, dtype: torch.dtype = torch.bfloat16) -> list[dict[str, object]]:
+    model = build_model(seed=seed, layers=layers, dtype=dtype)
+    results = []
+    for prompt_len in prompt_lens:
+        ids = make_prompt(prompt_len, model.config.vocab_size, seed=seed + prompt_len)
+        check = verify_against_torch(model, ids, variant=variant)
+        torch_time = time_ttft_ms(model, ids, warmup=warmup, iters=iters)
+        with patched_sdpa_with_gfx950(variant=variant):
+            ours_time = time_ttft_ms(model, ids, warmup=warmup, iters=iters)
+        row = {
+            "prompt_len": prompt_len,
+            "layers": model.config.num_hidden_layers,
+            "dtype": str(dtype).replace("torch.", ""),
+            "variant": variant,
+            "ttft_ms_gfx950": ours_time,
+            "ttft_ms_torch_sdpa": torch_time,
+            "speedup": torch_time["p50_ms"] / ours_time["p50_ms"],
+            "verification": check,
+        }
+        print(f"[ttft] S={prompt_len}: gfx950 {ours_time['p50_ms']:.2f} ms, torch SDPA {torch_time['p50_ms']:.2f} ms, "
+              f"max|dlogit|={check['max_abs_diff']:.3e} (torch default vs math: "
+              f"{check['noise_floor_torch_default_vs_math']:.3e}; |logit| <= {check['logit_abs_max']:.2f}), "
+              f"argmax_match={check['argmax_match']}", flush=True)
+        results.append(row)
+    return results
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--prompt-lens", type=int, nargs="+", default=[4096, 16384])
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--variant", default="sliced", choices=["basic", "optimized", "sliced"])
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--iters", type=int, default=5)
+    ap.add_argument("--json", default=None, help="write the results list to this file")
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("ttft_qwen.py needs a GPU (gfx950)", file=sys.stderr)
+        return 1
+    results = run(args.prompt_lens, layers=args.layers, seed=args.seed, variant=args.variant, warmup=args.warmup,
+                  iters=args.iters)
+    if args.json:
+        with open(args.json, "w") as fh:
+            json.dump(results, fh, indent=1)
+    ok = all(r["verification"]["argmax_match"] and r["verification"]["within_noise_floor"] for r in results)
+    return 0 if ok else 2
+
+
+if __name__ == "__main__":
+    sys.exit(main())
