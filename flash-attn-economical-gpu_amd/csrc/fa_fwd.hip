@@ -489,7 +489,8 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 2, 1),                  \
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 1, 0),                 \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 128, 1, 0),                 \
-  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 0)
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 0),                 \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 1)
 
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),

@@ -83,8 +83,13 @@ def fa_candidates(variant: int, dtype, D: int) -> list[FaTileChoice]:
     stages = stages_for(variant)
     for bm, bn, waves in FA_TILE_SPACE:
         choice = FaTileChoice(bm, bn, waves, stages, 1)
-        if hip_lib.fa_fwd_supported(variant, dtype, D, choice.to_c()):
-            out.append(choice)
+        if not hip_lib.fa_fwd_supported(variant, dtype, D, choice.to_c()):
+            continue
+        # the sliced variant may split KV at run time: its split instantiation must exist as well
+        if variant == hip_lib.FA_VARIANT_SLICED and not hip_lib.fa_fwd_supported(
+                variant, dtype, D, FaTileChoice(bm, bn, waves, stages, 2).to_c()):
+            continue
+        out.append(choice)
     return out
 
 

@@ -1,0 +1,152 @@
+"""Timed launch-configuration sweep for gfx950; writes tune_table.json.
+
+The reference's tuner compiles every candidate and keeps the feasible one with the largest resource
+footprint, without timing (tuner.py:489-560; mma.py:63-81 is a fixed table). Here every built tile
+that fits the device is timed on the device with HIP events, per shape bucket, and the winner is
+persisted; FlashAttentionTuner* and _select_2d_contiguous_config read the table
+(gfx950_configs.choose_fa_tile / choose_gemm_tile).
+
+  * attention: tiles (block_m, block_n, waves) x variant (basic / optimized / sliced) x dtype x D x
+    causal, per (B*H, M, N) power-of-two bucket;
+  * GEMM: tiles (block_m, block_n, block_k, waves) x GROUP_M in {4, 8, 16}, per (M, N, K) bucket.
+
+Usage: python gfx950_tune.py [--quick] [--out tune_table.json]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+import time
+
+import torch
+
+import gfx950_configs as cfgs
+import hip_lib
+
+VARIANTS = {"basic": hip_lib.FA_VARIANT_BASIC, "optimized": hip_lib.FA_VARIANT_OPT,
+            "sliced": hip_lib.FA_VARIANT_SLICED}
+
+# (name, dtype, B, H, H_kv, N, D, causal, variants) -- the BASELINE.json configurations
+FA_SWEEP = (
+    [("fp16_d128", torch.float16, 4, 32, 32, n, 128, c, ("basic", "optimized", "sliced"))
+     for n in (1024, 2048, 4096, 8192, 16384) for c in (False, True)]
+    + [("bf16_d256", torch.bfloat16, 2, 16, 16, n, 256, False, ("basic", "optimized", "sliced"))
+       for n in (1024, 2048, 4096, 8192)]
+    + [("fp16_d64_cfg1", torch.float16, 1, 4, 4, 512, 64, False, ("basic", "optimized", "sliced"))]
+    + [("ttft_bf16_gqa", torch.bfloat16, 1, 12, 2, n, 128, True, ("sliced", "optimized")) for n in (4096, 16384)]
+)
+GEMM_SWEEP = [(n, n, n) for n in (1024, 2048, 4096, 8192, 16384)] + [(8192, 8192, 256), (1024, 1024, 256)]
+GROUP_MS = (4, 8, 16)
+
+
+def _time(fn, warmup: int, iters: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
+
+
+def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5, log=print) -> None:
+    dev = torch.device("cuda:0")
+    for name, dtype, B, H, Hkv, N, D, causal, variants in sweep:
+        q = torch.randn(B, H, N, D, device=dev, dtype=dtype)
+        k = torch.randn(B, Hkv, N, D, device=dev, dtype=dtype)
+        v = torch.randn(B, Hkv, N, D, device=dev, dtype=dtype)
+        o = torch.empty_like(q)
+        flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
+        for vname in variants:
+            variant = VARIANTS[vname]
+            results = {}
+            for cand in cfgs.fa_candidates(variant, dtype, D):
+                splits = 1
+                ws = None
+                if variant == hip_lib.FA_VARIANT_SLICED:
+                    splits = cfgs.choose_splits(B, H, N, N, cand.block_m, cand.block_n)
+                    need = hip_lib.workspace_bytes(B, H, N, D, splits)
+                    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+                tile = cfgs.FaTileChoice(cand.block_m, cand.block_n, cand.waves, cand.stages, splits).to_c()
+                ms = _time(lambda: hip_lib.fa_fwd(q, k, v, o, None, sm_scale=D ** -0.5, causal=causal,
+                                                  variant=variant, tile=tile, workspace=ws), warmup, iters)
+                results[f"{cand.block_m}x{cand.block_n}x{cand.waves}"] = round(ms, 4)
+            best = min(results, key=results.get)
+            key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, N, N)
+            table["fa"][key] = {
+                "tile": [int(x) for x in best.split("x")],
+                "ms": results[best],
+                "tflops": round(flops / results[best] / 1e9, 1),
+                "timed": results,
+            }
+            log(f"[tune] attention {name} N={N} causal={causal} {vname}: best {best} "
+                f"{results[best]:.3f} ms ({flops / results[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
+        del q, k, v, o
+        torch.cuda.empty_cache()
+
+
+def tune_gemm(table: dict, sweep=GEMM_SWEEP, warmup: int = 2, iters: int = 5, log=print) -> None:
+    dev = torch.device("cuda:0")
+    for M, N, K in sweep:
+        a = (torch.rand(M, K, device=dev) * 2 - 1).half()
+        b = (torch.rand(K, N, device=dev) * 2 - 1).half()
+        c = torch.empty(M, N, device=dev, dtype=torch.float16)
+        results = {}
+        for t in cfgs.gemm_candidates():
+            if M % t[0] or N % t[1] or K % t[2]:
+                continue
+            for gm in GROUP_MS:
+                gt = hip_lib.GemmTile(t[0], t[1], t[2], t[3], gm)
+                results[f"{t[0]}x{t[1]}x{t[2]}x{t[3]}g{gm}"] = round(
+                    _time(lambda: hip_lib.gemm_f16(a, b, c, gt), warmup, iters), 4)
+        if not results:
+            continue
+        best = min(results, key=results.get)
+        tile_part, gm_part = best.split("g")
+        table["gemm"][cfgs.gemm_table_key(M, N, K)] = {
+            "tile": [int(x) for x in tile_part.split("x")],
+            "group_m": int(gm_part),
+            "ms": results[best],
+            "tflops": round(2.0 * M * N * K / results[best] / 1e9, 1),
+            "timed": results,
+        }
+        log(f"[tune] gemm {M}x{N}x{K}: best {best} {results[best]:.3f} ms "
+            f"({2.0 * M * N * K / results[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
+        del a, b, c
+        torch.cuda.empty_cache()
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--out", default=str(cfgs.TUNE_TABLE_PATH))
+    ap.add_argument("--quick", action="store_true", help="fewer timed launches per candidate")
+    ap.add_argument("--only", choices=["fa", "gemm"], default=None)
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("gfx950_tune.py needs a GPU", file=sys.stderr)
+        return 1
+    table = {"fa": {}, "gemm": {}}
+    t0 = time.time()
+    iters = 3 if args.quick else 5
+    if args.only in (None, "fa"):
+        tune_attention(table, iters=iters, log=lambda m: print(m, flush=True))
+    if args.only in (None, "gemm"):
+        tune_gemm(table, iters=iters, log=lambda m: print(m, flush=True))
+    table["meta"] = {"device": torch.cuda.get_device_name(0), "seconds": round(time.time() - t0, 1),
+                     "torch": torch.__version__, "iters": iters}
+    with open(args.out, "w") as fh:
+        json.dump(table, fh, indent=1, sort_keys=True)
+        fh.write("\n")
+    print(f"[tune] wrote {args.out}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,117 @@
+"""Persisted tuning table (the gfx950 replacement for the reference's untimed candidate ranking,
+tuner.py:489-560 and mma.py:63-81): the committed table only names built tiles, selection honours
+it, a missing table falls back to the preference order, and on the GPU a small live sweep writes
+entries that selection then returns."""
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+import gfx950_configs as cfgs
+import gfx950_tune
+import hip_lib
+import mma
+
+_DTYPES = {"f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _parse_fa_key(key: str):
+    v, dt, d, c, bh, m, n = key.split("|")
+    return int(v[1:]), _DTYPES[dt], int(d[1:]), bool(int(c[1:])), int(bh[2:]), int(m[1:]), int(n[1:])
+
+
+@pytest.fixture
+def fresh_table_cache():
+    cfgs.reset_tune_table_cache()
+    yield
+    cfgs.reset_tune_table_cache()
+
+
+def test_committed_table_names_only_built_tiles(fresh_table_cache):
+    table = cfgs.load_tune_table()
+    assert table["fa"] and table["gemm"], "tune_table.json is missing or empty"
+    for key, entry in table["fa"].items():
+        variant, dtype, D, _causal, _bh, _m, _n = _parse_fa_key(key)
+        tiles = {(c.block_m, c.block_n, c.waves) for c in cfgs.fa_candidates(variant, dtype, D)}
+        assert tuple(entry["tile"]) in tiles, key
+        timed = entry["timed"]
+        best = "x".join(map(str, entry["tile"]))
+        assert timed[best] == entry["ms"] == min(timed.values()), key
+    gemm_tiles = set(cfgs.gemm_candidates())
+    for key, entry in table["gemm"].items():
+        assert tuple(entry["tile"]) in gemm_tiles, key
+        assert entry["group_m"] in gfx950_tune.GROUP_MS
+        assert entry["ms"] == min(entry["timed"].values()), key
+
+
+def test_selection_returns_the_table_winner(fresh_table_cache):
+    table = cfgs.load_tune_table()
+    for key, entry in table["fa"].items():
+        variant, dtype, D, causal, bh, m, n = _parse_fa_key(key)
+        cands = cfgs.fa_candidates(variant, dtype, D)
+        got = cfgs.choose_fa_tile(variant, dtype, D, causal, 1, bh, m, n, cands)
+        assert [got.block_m, got.block_n, got.waves] == entry["tile"], key
+    for key, entry in table["gemm"].items():
+        M, N, K = (int(p[1:]) for p in key.split("|"))
+        try:
+            bm, bn, bk, waves, gm = cfgs.choose_gemm_tile(M, N, K)
+        except ValueError:
+            continue
+        assert [bm, bn, bk, waves] == entry["tile"] and gm == entry["group_m"], key
+        # the drop-in selector reports the same tile (reference tuple order)
+        assert mma._select_2d_contiguous_config(M, N, K)[:4] == (bm, bn, bk, gm)
+
+
+def test_shapes_in_one_bucket_share_an_entry():
+    k1 = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192)
+    k2 = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 2, 64, 5000, 7000)
+    k3 = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, True, 4, 32, 8192, 8192)
+    assert k1 == k2 != k3
+    assert cfgs.gemm_table_key(8192, 8192, 8192) == cfgs.gemm_table_key(5000, 8000, 4097)
+
+
+def test_missing_table_falls_back_to_preference_order(tmp_path, monkeypatch, fresh_table_cache):
+    monkeypatch.setattr(cfgs, "TUNE_TABLE_PATH", tmp_path / "absent.json")
+    cands = cfgs.fa_candidates(hip_lib.FA_VARIANT_BASIC, torch.float16, 128)
+    got = cfgs.choose_fa_tile(hip_lib.FA_VARIANT_BASIC, torch.float16, 128, False, 4, 32, 8192, 8192, cands)
+    assert got == cands[0]
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192) == (*cfgs.gemm_candidates()[0], cfgs.GEMM_DEFAULT_GROUP_M)
+
+
+def test_table_entry_for_unbuilt_tile_is_ignored(tmp_path, monkeypatch, fresh_table_cache):
+    key = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192)
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"fa": {key: {"tile": [512, 512, 16]}},
+                                "gemm": {cfgs.gemm_table_key(8192, 8192, 8192): {"tile": [1, 2, 3, 4], "group_m": 4}}}))
+    monkeypatch.setattr(cfgs, "TUNE_TABLE_PATH", path)
+    cands = cfgs.fa_candidates(hip_lib.FA_VARIANT_OPT, torch.float16, 128)
+    assert cfgs.choose_fa_tile(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192, cands) == cands[0]
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192)[:4] == cfgs.gemm_candidates()[0]
+
+
+def test_sliced_candidates_have_split_kernels():
+    for dtype in (torch.float16, torch.bfloat16):
+        for D in (64, 128, 256):
+            for c in cfgs.fa_candidates(hip_lib.FA_VARIANT_SLICED, dtype, D):
+                split = cfgs.FaTileChoice(c.block_m, c.block_n, c.waves, c.stages, 4).to_c()
+                assert hip_lib.fa_fwd_supported(hip_lib.FA_VARIANT_SLICED, dtype, D, split), (dtype, D, c)
+
+
+@pytest.mark.gpu
+def test_live_sweep_writes_selectable_entries(gpu, tmp_path, monkeypatch, fresh_table_cache):
+    print("[tune] live sweep: fp16 D=64 B1 H4 N=512, gemm 256x256x256", flush=True)
+    table = {"fa": {}, "gemm": {}}
+    sweep = [("t", torch.float16, 1, 4, 4, 512, 64, False, ("basic", "sliced"))]
+    gfx950_tune.tune_attention(table, sweep=sweep, warmup=1, iters=2, log=lambda m: None)
+    gfx950_tune.tune_gemm(table, sweep=[(256, 256, 256)], warmup=1, iters=2, log=lambda m: None)
+    assert len(table["fa"]) == 2 and len(table["gemm"]) == 1
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(table))
+    monkeypatch.setattr(cfgs, "TUNE_TABLE_PATH", path)
+    for key, entry in table["fa"].items():
+        variant, dtype, D, causal, bh, m, n = _parse_fa_key(key)
+        got = cfgs.choose_fa_tile(variant, dtype, D, causal, 1, bh, m, n, cfgs.fa_candidates(variant, dtype, D))
+        assert [got.block_m, got.block_n, got.waves] == entry["tile"]
+    assert list(cfgs.choose_gemm_tile(256, 256, 256)[:4]) == table["gemm"][cfgs.gemm_table_key(256, 256, 256)]["tile"]
