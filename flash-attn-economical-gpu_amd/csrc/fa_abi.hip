@@ -62,7 +62,12 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
   return nullptr;
 }
 
-int stages_of(int variant) { return variant == FA_VARIANT_BASIC ? 1 : 2; }
+// Pipeline of a launch: basic keeps one K/V buffer (1); optimized and sliced double-buffer K/V (2),
+// or, when the tile asks for stages=3, also run the two wave groups half a tile apart (ping-pong).
+int stages_of(int variant, const fa_tile* t) {
+  if (variant == FA_VARIANT_BASIC) return 1;
+  return (t != nullptr && t->stages == 3) ? 3 : 2;
+}
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.
 const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_tile* t, bool* split_out,
@@ -92,12 +97,12 @@ const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_til
   const bool split = splits > 1;
   *split_out = split;
   const fa::FaKernelEntry* e =
-      find_fwd(stages_of(variant), dtype, D, t->waves, t->block_m / t->waves, t->block_n, split ? 1 : 0);
+      find_fwd(stages_of(variant, t), dtype, D, t->waves, t->block_m / t->waves, t->block_n, split ? 1 : 0);
   if (e == nullptr)
     *code = fail(FA_ENOTSUP,
                  "attention tile block_m=%d block_n=%d waves=%d stages=%d split=%d is not built for "
                  "dtype=%d D=%d",
-                 t->block_m, t->block_n, t->waves, stages_of(variant), split ? 1 : 0, dtype, D);
+                 t->block_m, t->block_n, t->waves, stages_of(variant, t), split ? 1 : 0, dtype, D);
   return e;
 }
 
@@ -190,6 +195,17 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
     const int64_t rows = (int64_t)splits * a->B * a->H * a->M;
     p.ws_o = static_cast<float*>(a->workspace);
     p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + ((rows * a->D * 4 + 255) & ~(int64_t)255));
+  }
+
+  if (e->stages == 3) {
+    // The pipelined kernel addresses one (batch, kv-head) row range [0, N + block_n) of K and V
+    // with 32-bit byte offsets and relies on whole rows for its tail check: fall back to the
+    // double-buffered kernel of the same tile when that does not hold.
+    const int64_t span = ((int64_t)a->N + bn) * 2 * (a->k_stride[2] > a->v_stride[2] ? a->k_stride[2] : a->v_stride[2]);
+    if (span > 0xffffffffLL || a->k_stride[2] < a->D || a->v_stride[2] < a->D) {
+      e = find_fwd(2, a->dtype, a->D, e->waves, e->rows_per_wave, e->block_n, e->split);
+      if (e == nullptr) return fail(FA_ENOTSUP, "no double-buffered fallback for the pipelined attention tile");
+    }
   }
 
   hipStream_t s = static_cast<hipStream_t>(stream);

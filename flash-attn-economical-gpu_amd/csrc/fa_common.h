@@ -94,6 +94,50 @@ __device__ inline float xhalf_sum(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer resource (the four descriptor words) over [base, base + bytes): buffer loads address
+// it with a 32-bit per-lane byte offset and return zeros for offsets at or past `bytes` (the
+// hardware range check), so tiles that run past the end of a sequence need no branch. Word 1
+// carries stride 0 (raw buffer); 0x00020000 is the gfx9-family word 3 for untyped 32-bit data.
+// Callers pass wave-uniform values; readfirstlane puts them in scalar registers.
+__device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// 16 bytes per lane from the buffer straight into LDS (buffer_load_dwordx4 ... lds): lane i writes
+// lds_block[16 i .. 16 i + 15], so one wave instruction fills one contiguous 1 KiB block (M0 holds
+// the wave-uniform block address). Completion is tracked by vmcnt. The instruction is issued from
+// inline asm so that the compiler, which cannot tell the ring slots apart, does not wait for every
+// LDS-DMA in flight before each LDS read; the kernel waits explicitly (wait_vm_lds_barrier).
+// vmcnt retires in order, so the compiler's own vmcnt waits stay correct (they can only wait
+// longer when these loads are outstanding).
+__device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, const void* lds_block) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_block);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+               :
+               : "v"(byte_off), "s"(lds), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding and all its LDS
+// operations are done, then barrier. Unlike __syncthreads() this does not wait for every
+// outstanding load: LDS-DMA loads issued for later steps stay in flight across the barrier.
+// (gfx9 s_waitcnt encoding: vmcnt [3:0] and [15:14], expcnt [6:4] (7 = no wait), lgkmcnt [11:8].)
+template <int N>
+__device__ inline void wait_vm_lds_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Workgroup id remapped so that consecutive logical ids land on the same XCD. Workgroups are
 // dispatched round-robin over the 8 XCDs of MI355X; logical id L = xcd * per + slot keeps
 // neighbouring tiles (which share K/V or A/B panels) inside one XCD's L2.

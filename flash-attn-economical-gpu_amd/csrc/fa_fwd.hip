@@ -137,36 +137,47 @@ struct FwdKernel {
     }
   }
 
-  // Masks (only on tiles that need them), online softmax with lazy rescale, P packing. Leaves
-  // packed P in pk.
-  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][RT], floatx16 (&acc)[DTL][RT], float (&m_use)[RT],
-                                        float (&l_i)[RT], int n0, int wrow0, int col, int hh, const FwdParams& p) {
-    const float c = p.c;
-    const bool need_mask = (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
-    if (need_mask) {
+  // Keys past N, and (causal) keys after the query row, get score -inf. Wave-uniform test first:
+  // only tiles at the sequence end or on the diagonal need the per-element masks.
+  __device__ static inline bool tile_needs_mask(int n0, int wrow0, const FwdParams& p) {
+    return (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
+  }
+  __device__ static inline void mask_tile(STile& s, int n0, int wrow0, int col, int hh, const FwdParams& p) {
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt)
+    for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const int i = wrow0 + rt * 32 + col;
+      for (int rt = 0; rt < RT; ++rt) {
+        const int i = wrow0 + rt * 32 + col;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int j = n0 + jt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (j >= p.N || (p.causal && j > i)) s[jt][rt][r] = FA_NEG_INF;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int j = n0 + jt * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (j >= p.N || (p.causal && j > i)) s[jt][rt][r] = FA_NEG_INF;
         }
-    }
+      }
+  }
+
+  // Row max of a score tile (each lane's row, both half-waves).
+  __device__ static inline void tile_max(const STile& s, float (&mx)[RT]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float mx = FA_NEG_INF;
+      float m = FA_NEG_INF;
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[jt][rt][r], s[jt][rt][r + 1]));
-      mx = xhalf_max(mx);
-      const bool need = mx > m_use[rt] + THRESH / c;
+        for (int r = 0; r < 16; r += 2) m = fmaxf(m, fmaxf(s[jt][rt][r], s[jt][rt][r + 1]));
+      mx[rt] = xhalf_max(m);
+    }
+  }
+
+  // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some row of the
+  // wave sees a max more than THRESH (log2 units) above it.
+  __device__ static inline void rescale(const float (&mx)[RT], floatx16 (&acc)[DTL][RT], float (&m_use)[RT],
+                                        float (&l_i)[RT], float c) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const bool need = mx[rt] > m_use[rt] + THRESH / c;
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        const float m_new = fmaxf(m_use[rt], mx);
+        const float m_new = fmaxf(m_use[rt], mx[rt]);
         const float alpha = (m_use[rt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[rt] - m_new) * c);
         m_use[rt] = m_new;
         l_i[rt] *= alpha;
@@ -175,6 +186,26 @@ struct FwdKernel {
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[dt][rt][r] *= alpha;
       }
+    }
+  }
+
+  // Masks (only on tiles that need them), online softmax with lazy rescale, P packing. Leaves
+  // packed P in pk.
+  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][RT], floatx16 (&acc)[DTL][RT], float (&m_use)[RT],
+                                        float (&l_i)[RT], int n0, int wrow0, int col, int hh, const FwdParams& p) {
+    if (tile_needs_mask(n0, wrow0, p)) mask_tile(s, n0, wrow0, col, hh, p);
+    float mx[RT];
+    tile_max(s, mx);
+    rescale(mx, acc, m_use, l_i, p.c);
+    exp_pack(s, pk, m_use, l_i, p.c);
+  }
+
+  // P = exp2(S c - m_use c) rounded to the input dtype and packed as the B operand of P V; the
+  // row sum l accumulates the same P.
+  __device__ static inline void exp_pack(const STile& s, u32x4 (&pk)[KC][RT], const float (&m_use)[RT],
+                                         float (&l_i)[RT], float c) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
       const float mc = (m_use[rt] == FA_NEG_INF) ? 0.f : m_use[rt] * c;
       float l0 = 0.f, l1 = 0.f;
 #pragma unroll
@@ -223,6 +254,80 @@ struct FwdKernel {
     }
   }
 
+  // Software-pipelined step (stages=3), first half: the QK MFMAs of the next tile interleaved
+  // with the exp / pack / row-sum VALU work of the current tile, a few VALU ops per MFMA, so the
+  // matrix core and the VALU run at the same time inside one wave.
+  static constexpr int kExpValu = JT * RT * (16 * 2 + 8 * 2);  // FMA + exp per score, pack + sum per pair
+  static constexpr int kXValuPerMfma = (kExpValu + DC * JT - 1) / (DC * JT);  // per group of RT MFMAs
+  __device__ static inline void x_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, kReadAheadK, 2);
+#pragma unroll
+    for (int i = 0; i < DC * JT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, kXValuPerMfma, 2);
+    }
+  }
+  // Second half: the PV MFMAs of the current tile interleaved with the row max of the next one.
+  __device__ static inline void y_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kReadAheadV, 2);
+#pragma unroll
+    for (int i = 0; i < KC * DTL; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+    }
+  }
+
+  // ---- stages=3: fragment-major LDS tiles filled by LDS-DMA ----
+  // K tile: NKB blocks of 1 KiB, block (jt, cc) = jt * DC + cc holds, at byte 16 l, the 16 bytes
+  // lane l feeds to the QK MFMA: K[jt*32 + (l & 31)][cc*16 + 8*(l >> 5) .. +7].
+  // V tile: NVB blocks of 1 KiB, block (kc, dt) = kc * DTL + dt holds the two transposing reads
+  // (rows kc*16 + 0..7, then + 8..15) of that (key chunk, d tile), lane L's 8 bytes at 8 L.
+  // Every LDS read instruction thus reads one contiguous block (no bank conflicts, no per-lane
+  // address arithmetic), and every DMA instruction writes one block.
+  static constexpr int NKB = JT * DC;
+  static constexpr int NVB = KC * DTL;
+  static constexpr int KT_ELEMS = NKB * 512;  // 16-bit elements per K tile
+  static constexpr int VT_ELEMS = NVB * 512;
+  static constexpr int RING = (WAVES >= 8) ? 3 : 2;  // tiles of K (and of V) resident in LDS
+  static constexpr int NKW = NKB / WAVES;            // DMA blocks per wave per K tile
+  static constexpr int NVW = NVB / WAVES;
+  static_assert(STAGES != 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
+
+  __device__ static inline void qk_fm(STile& s, const u32x4 (&qf)[RT][DC], const uint16_t* kslot_lane) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[jt][rt][r] = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc) {
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(kslot_lane + (jt * DC + cc) * 512);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s[jt][rt] = T::mfma32(kf, qf[rt][cc], s[jt][rt]);
+      }
+    }
+  }
+
+  __device__ static inline void pv_fm(floatx16 (&acc)[DTL][RT], const u32x4 (&pk)[KC][RT], const uint16_t* vslot_lane) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) {
+        const uint16_t* base = vslot_lane + (kc * DTL + dt) * 512;
+        const u32x2 lo = lds_read_tr16(base);
+        const u32x2 hi = lds_read_tr16(base + 256);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = T::mfma32(vf, pk[kc][rt], acc[dt][rt]);
+      }
+    }
+  }
+
   // O^T += V^T P^T
   __device__ static inline void pv(floatx16 (&acc)[DTL][RT], const u32x4 (&pk)[KC][RT], const uint16_t* vs,
                                    int lane_v_off) {
@@ -241,7 +346,9 @@ struct FwdKernel {
   }
 
   __device__ static void run(const FwdParams& p) {
-    constexpr int SMEM = (STAGES == 1) ? (KTILE + VTILE) : 2 * (KTILE + VTILE);
+    constexpr int SMEM = (STAGES == 1)   ? (KTILE + VTILE)
+                         : (STAGES == 2) ? 2 * (KTILE + VTILE)
+                                         : RING * (KT_ELEMS + VT_ELEMS);
     __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
 
     const int tid = threadIdx.x;
@@ -335,6 +442,121 @@ struct FwdKernel {
           softmax(s, pk, acc, m_use, l_i, n0, wrow0, col, hh, p);
           pv(acc, pk, vs, lane_v_off);
           pv_schedule();
+        }
+      }
+    } else if (STAGES == 3) {
+      // Software pipeline across KV tiles inside each wave. Step u starts with S_u = K_u Q^T and
+      // its row max already computed, then
+      //   (rare branch) lazy rescale for tile u
+      //   X: P_u = exp(S_u)      interleaved with  S_{u+1} = K_{u+1} Q^T      (VALU | MFMA)
+      //   Y: O += P_u V_u        interleaved with  rowmax(S_{u+1})             (MFMA | VALU)
+      // K runs one tile ahead of V: step u reads K_{u+1} and V_u. Tiles reach LDS by LDS-DMA
+      // (buffer_load ... lds, no registers) into rings of RING K slots and RING V slots: step u
+      // issues K_{u+RING} into the slot K_u left and V_{u+RING-1} into the slot V_{u-1} left, so
+      // with RING = 3 a tile has two steps to arrive; the barrier at the end of a step waits only
+      // for the loads the next step reads. The buffer range is the (b, kv-head) rows [0, N): rows
+      // past N read as zero without a branch (the host keeps (N + block_n) * row stride * 2 bytes
+      // below 2^32). The step is unrolled by two so the two score tiles alternate without copies.
+      uint16_t* kring = smem;
+      uint16_t* vring = smem + RING * KT_ELEMS;
+      const auto krs = make_rsrc(p.k + (int64_t)b * p.sk0 + (int64_t)hk * p.sk1, (uint32_t)p.N * (uint32_t)p.sk2 * 2u);
+      const auto vrs = make_rsrc(p.v + (int64_t)b * p.sv0 + (int64_t)hk * p.sv1, (uint32_t)p.N * (uint32_t)p.sv2 * 2u);
+      // Byte offsets (within a tile) of the 16 bytes this lane moves for each block of this wave.
+      uint32_t koffs[NKW], voffs[NVW];
+#pragma unroll
+      for (int j = 0; j < NKW; ++j) {
+        const int blk = wave * NKW + j, jt = blk / DC, cc = blk % DC;
+        const uint32_t row = jt * 32 + (lane & 31), c0 = cc * 16 + 8 * (lane >> 5);
+        koffs[j] = (row * (uint32_t)p.sk2 + c0) * 2u;
+      }
+#pragma unroll
+      for (int j = 0; j < NVW; ++j) {
+        const int blk = wave * NVW + j, kc = blk / DTL, dt = blk % DTL;
+        const int m = lane & 31, half = lane >> 5;  // the lane pair (2m, 2m+1) of read `half`
+        const uint32_t row = kc * 16 + 8 * half + 4 * (m >> 4) + ((m & 7) >> 1);
+        const uint32_t c0 = dt * 32 + 16 * ((m >> 3) & 1) + 8 * (m & 1);
+        voffs[j] = (row * (uint32_t)p.sv2 + c0) * 2u;
+      }
+      auto issue_k = [&](int u) {
+        if (u >= ntiles) return;
+        const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
+        uint16_t* slot = kring + (u % RING) * KT_ELEMS;
+#pragma unroll
+        for (int j = 0; j < NKW; ++j) buffer_load16_to_lds(krs, koffs[j] + toff, slot + (wave * NKW + j) * 512);
+      };
+      auto issue_v = [&](int u) {
+        if (u >= ntiles) return;
+        const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
+        uint16_t* slot = vring + (u % RING) * VT_ELEMS;
+#pragma unroll
+        for (int j = 0; j < NVW; ++j) buffer_load16_to_lds(vrs, voffs[j] + toff, slot + (wave * NVW + j) * 512);
+      };
+      const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
+      const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
+      STile sa, sb;
+      float mxa[RT], mxb[RT];
+      if (ntiles > 0) {
+#pragma unroll
+        for (int i = 0; i < RING; ++i) {
+          issue_k(i);
+          if (i + 1 < RING) issue_v(i);
+        }
+        wait_vm_lds_barrier<0>();
+        qk_fm(sa, qf, klane);
+        qk_schedule();
+        tile_max(sa, mxa);           // masks, if tile 0 needs them, come in step 0
+        wait_vm_lds_barrier<0>();    // every wave is done with K slot 0 before step 0 refills it
+      }
+      // Masks for tile u (rare: sequence end, causal diagonal) and the row max they change. The
+      // steady-state step computes the max of the next tile unmasked, inside the same basic block
+      // as its MFMAs; tiles that need masks redo it here.
+      auto fix_masked = [&](STile& cur, float (&mx_cur)[RT], int u) {
+        const int n0 = (t_begin + u) * BN;
+        if (tile_needs_mask(n0, wrow0, p)) {
+          mask_tile(cur, n0, wrow0, col, hh, p);
+          tile_max(cur, mx_cur);
+        }
+      };
+      // Step u of a tile that has a successor (u + 1 < ntiles).
+      auto step = [&](STile& cur, float (&mx_cur)[RT], STile& nxt, float (&mx_nxt)[RT], int u) {
+        issue_k(u + RING);      // into K_u's slot (read in step u-1)
+        issue_v(u + RING - 1);  // into V_{u-1}'s slot (read in step u-1)
+        fix_masked(cur, mx_cur, u);
+        rescale(mx_cur, acc, m_use, l_i, p.c);
+        u32x4 pk[KC][RT];
+        exp_pack(cur, pk, m_use, l_i, p.c);
+        qk_fm(nxt, qf, klane + ((u + 1) % RING) * KT_ELEMS);
+        x_schedule();
+        pv_fm(acc, pk, vlane + (u % RING) * VT_ELEMS);
+        tile_max(nxt, mx_nxt);
+        y_schedule();
+        // Step u+1 reads K_{u+2} and V_{u+1}. With RING = 3 they were issued in step u-1 (or
+        // before the loop), and this step's loads may stay in flight.
+        if (RING > 2 && u + RING < ntiles)
+          wait_vm_lds_barrier<NKW + NVW>();
+        else
+          wait_vm_lds_barrier<0>();
+      };
+      // The last tile: no successor to overlap with.
+      auto last = [&](STile& cur, float (&mx_cur)[RT], int u) {
+        fix_masked(cur, mx_cur, u);
+        rescale(mx_cur, acc, m_use, l_i, p.c);
+        u32x4 pk[KC][RT];
+        exp_pack(cur, pk, m_use, l_i, p.c);
+        pv_fm(acc, pk, vlane + (u % RING) * VT_ELEMS);
+        pv_schedule();
+      };
+      if (ntiles > 0) {
+        int u = 0;
+        for (; u + 2 < ntiles; u += 2) {
+          step(sa, mxa, sb, mxb, u);
+          step(sb, mxb, sa, mxa, u + 1);
+        }
+        if (u + 1 < ntiles) {
+          step(sa, mxa, sb, mxb, u);
+          last(sb, mxb, u + 1);
+        } else {
+          last(sa, mxa, u);
         }
       }
     } else {
@@ -490,7 +712,11 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 1, 0),                 \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 128, 1, 0),                 \
   FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 0),                 \
-  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 1)
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 128, 2, 1),                 \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 3, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 3, 1),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 1)
 
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),

@@ -31,16 +31,35 @@ VARIANT_BY_KERNEL = {
 }
 
 # Attention tiles in preference order (used when the tuning table has no entry for a shape):
-# (block_m, block_n, waves). stages follow the variant (basic 1, optimized/sliced 2).
+# (block_m, block_n, waves, stages). stages selects the kernel pipeline:
+#   1  one K/V buffer, two barriers per KV tile (the basic variant),
+#   2  double-buffered K/V, one barrier per tile,
+#   3  software-pipelined (QK of tile u+1 overlapped with the softmax of tile u inside each wave,
+#      K/V brought into an LDS ring by LDS-DMA loads).
+# The basic variant uses stages 1; optimized and sliced use 3 or 2.
 FA_TILE_SPACE = [
-    (256, 64, 8),
-    (256, 64, 4),
-    (128, 64, 4),
-    (256, 128, 8),
-    (128, 128, 4),
-    (256, 32, 8),
-    (128, 32, 4),
+    (128, 64, 4, 3),
+    (256, 64, 8, 3),
+    (256, 64, 8, 2),
+    (256, 64, 4, 2),
+    (128, 64, 4, 2),
+    (256, 128, 8, 2),
+    (128, 128, 4, 2),
+    (256, 32, 8, 2),
+    (128, 32, 4, 2),
+    (256, 64, 8, 1),
+    (256, 64, 4, 1),
+    (128, 64, 4, 1),
+    (256, 128, 8, 1),
+    (128, 128, 4, 1),
+    (256, 32, 8, 1),
+    (128, 32, 4, 1),
 ]
+STAGES_BY_VARIANT = {
+    hip_lib.FA_VARIANT_BASIC: (1,),
+    hip_lib.FA_VARIANT_OPT: (3, 2),
+    hip_lib.FA_VARIANT_SLICED: (3, 2),
+}
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).
 GEMM_TILE_SPACE = [
@@ -74,14 +93,18 @@ class FaTileChoice:
 
 
 def stages_for(variant: int) -> int:
+    """Default pipeline of a variant when no tile is chosen (the double-buffered one for
+    optimized and sliced: it is built for every head dim)."""
     return 1 if variant == hip_lib.FA_VARIANT_BASIC else 2
 
 
 def fa_candidates(variant: int, dtype, D: int) -> list[FaTileChoice]:
     """Built attention tiles for (variant, dtype, D), in preference order."""
     out = []
-    stages = stages_for(variant)
-    for bm, bn, waves in FA_TILE_SPACE:
+    allowed = STAGES_BY_VARIANT.get(variant, ())
+    for bm, bn, waves, stages in FA_TILE_SPACE:
+        if stages not in allowed:
+            continue
         choice = FaTileChoice(bm, bn, waves, stages, 1)
         if not hip_lib.fa_fwd_supported(variant, dtype, D, choice.to_c()):
             continue
@@ -178,8 +201,9 @@ def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M:
     """Timed-table winner among candidates if recorded, else the first candidate (preference order)."""
     entry = load_tune_table()["fa"].get(fa_table_key(variant, dtype, D, causal, B, H, M, N))
     if entry is not None:
+        want = tuple(entry["tile"])
         for c in candidates:
-            if (c.block_m, c.block_n, c.waves) == tuple(entry["tile"]):
+            if (c.block_m, c.block_n, c.waves, c.stages)[:len(want)] == want:
                 return c
     return candidates[0]
 

@@ -6,7 +6,7 @@ that fits the device is timed on the device with HIP events, per shape bucket, a
 persisted; FlashAttentionTuner* and _select_2d_contiguous_config read the table
 (gfx950_configs.choose_fa_tile / choose_gemm_tile).
 
-  * attention: tiles (block_m, block_n, waves) x variant (basic / optimized / sliced) x dtype x D x
+  * attention: tiles (block_m, block_n, waves, stages) x variant (basic / optimized / sliced) x dtype x D x
     causal, per (B*H, M, N) power-of-two bucket;
   * GEMM: tiles (block_m, block_n, block_k, waves) x GROUP_M in {4, 8, 16}, per (M, N, K) bucket.
 
@@ -77,7 +77,7 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
                 tile = cfgs.FaTileChoice(cand.block_m, cand.block_n, cand.waves, cand.stages, splits).to_c()
                 ms = _time(lambda: hip_lib.fa_fwd(q, k, v, o, None, sm_scale=D ** -0.5, causal=causal,
                                                   variant=variant, tile=tile, workspace=ws), warmup, iters)
-                results[f"{cand.block_m}x{cand.block_n}x{cand.waves}"] = round(ms, 4)
+                results[f"{cand.block_m}x{cand.block_n}x{cand.waves}x{cand.stages}"] = round(ms, 4)
             best = min(results, key=results.get)
             key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, N, N)
             table["fa"][key] = {

@@ -247,13 +247,17 @@ class FlashAttentionTuner(Tuner):
     # -- resources ------------------------------------------------------------------------------
 
     def estimate_flash_fwd_shared_bytes(self, *, block_m: int, block_n_pad: int, block_dmodel: int,
-                                        element_size: int, stages: int | None = None) -> int:
-        """LDS of one gfx950 workgroup: per stage a K tile [block_n][D+8] and a V^T tile
-        [D][block_n+8] (the +8 elements are the 16-byte bank-skew pads). block_m does not enter:
-        Q stays in registers."""
+                                        element_size: int, stages: int | None = None,
+                                        num_warps: int | None = None) -> int:
+        """LDS of one gfx950 workgroup. stages 1/2: per buffer a K tile [block_n][D+8] and a V tile
+        [block_n][D+32] (the pads are bank skews). stages 3: a ring of 3 (8 waves) or 2 (fewer)
+        unpadded K and V tiles. block_m does not enter: Q stays in registers."""
         stages = cfgs.stages_for(self.variant) if stages is None else stages
         del block_m
-        return stages * element_size * (block_n_pad * (block_dmodel + 8) + block_dmodel * (block_n_pad + 8))
+        if stages == 3:
+            ring = 3 if (num_warps or 0) >= 8 else 2
+            return ring * element_size * 2 * block_n_pad * block_dmodel
+        return stages * element_size * (block_n_pad * (block_dmodel + 8) + block_n_pad * (block_dmodel + 32))
 
     def _dtype_from_size(self, q: torch.Tensor | None = None) -> torch.dtype:
         if q is not None:
@@ -361,6 +365,8 @@ class FlashAttentionTuner(Tuner):
                     block_n_pad=int(config["BLOCK_N_PAD"]),
                     block_dmodel=self.D,
                     element_size=q.element_size(),
+                    stages=int(config["num_stages"]),
+                    num_warps=int(config["num_warps"]),
                 ),
                 dtype=q.dtype,
                 config=config,
@@ -560,6 +566,8 @@ class FlashAttentionBlockDNomaskTuner(FlashAttentionTuner):
                     block_n_pad=int(config["BLOCK_N_PAD"]),
                     block_dmodel=self.D,
                     element_size=self.dtype_size,
+                    stages=int(config["num_stages"]),
+                    num_warps=int(config["num_warps"]),
                 ),
                 dtype=q.dtype,
                 config=config,

@@ -25,6 +25,9 @@ TILES = {
     "opt128": (OPT, 128, 64, 4, 2),
     "opt256w4": (OPT, 256, 64, 4, 2),
     "opt256w8": (OPT, 256, 64, 8, 2),
+    # software-pipelined kernel (stages=3): LDS-DMA ring of 2 tiles (4 waves) or 3 tiles (8 waves)
+    "pipe128": (OPT, 128, 64, 4, 3),
+    "pipe256": (OPT, 256, 64, 8, 3),
 }
 
 
@@ -62,7 +65,63 @@ CASES = [
     ("ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "opt256w8"),
     ("tiny", 1, 1, 1, 1, 1, 64, F16, False, "basic128"),
     ("m_ne_n_causal", 1, 2, 2, 100, 260, 64, BF16, True, "opt128"),
+    ("pipe_d128", 1, 2, 2, 512, 512, 128, F16, False, "pipe128"),
+    ("pipe_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "pipe128"),
+    ("pipe_d64", 2, 2, 2, 256, 448, 64, F16, False, "pipe128"),
+    ("pipe_w8_d128_causal", 2, 2, 2, 512, 512, 128, F16, True, "pipe256"),
+    ("pipe_w8_d64_bf16", 1, 3, 3, 256, 576, 64, BF16, False, "pipe256"),
+    ("pipe_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "pipe128"),
+    ("pipe_ragged", 2, 3, 3, 200, 333, 128, F16, False, "pipe128"),
+    ("pipe_w8_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "pipe256"),
+    ("pipe_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pipe256"),
 ]
+
+
+@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256"])
+@pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320])
+def test_fa_pipelined_tile_counts(gpu, tile_name, n):
+    """1..5 KV tiles: the pipelined loop's prologue, unrolled pairs, peeled last tile and the
+    LDS-DMA ring (2 or 3 slots) at every length parity, with a partial last tile."""
+    print(f"[fa_abi] pipelined tile counts {tile_name} N={n}", flush=True)
+    B, H, M, D = 1, 2, 96, 128
+    q, k, v = make_qkv(300 + n, B, H, H, M, n, D, F16)
+    o, lse = run_fa(q, k, v, variant=None, tile=TILES[tile_name], causal=False)
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=False)
+    assert max_abs(o, o_ref) <= ATOL[F16]
+    assert max_abs(lse, lse_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("tile_name", ["opt256w8", "pipe128", "pipe256"])
+def test_fa_strided_bshd_layout(gpu, tile_name):
+    """q/k/v/o as [B, S, H, D] memory viewed as [B, H, S, D] (row stride H*D): buffer ranges and
+    DMA offsets of the pipelined kernel follow the strides."""
+    B, H, M, N, D = 2, 4, 160, 300, 128
+    print(f"[fa_abi] strided BSHD {tile_name}", flush=True)
+    q, k, v = make_qkv(911, B, H, H, M, N, D, F16)
+    dev = "cuda:0"
+    qd, kd, vd = (to_device(np.ascontiguousarray(x.transpose(0, 2, 1, 3)), F16, dev).transpose(1, 2) for x in (q, k, v))
+    od = torch.empty((B, M, H, D), dtype=F16, device=dev).transpose(1, 2)
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=dev)
+    var, bm, bn, waves, stages = TILES[tile_name]
+    hip_lib.fa_fwd(qd, kd, vd, od, lse, sm_scale=D ** -0.5, causal=True, variant=var,
+                   tile=hip_lib.make_tile(bm, bn, waves, stages, 1))
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=True)
+    assert max_abs(od.float().cpu().numpy(), o_ref) <= ATOL[F16]
+    assert max_abs(lse.cpu().numpy(), lse_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("splits", [2, 5])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
+    B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, BF16
+    print(f"[fa_abi] sliced pipelined splits={splits} causal={causal}", flush=True)
+    q, k, v = make_qkv(78, B, H, Hkv, M, N, D, dtype)
+    for tile_name in ("pipe128", "pipe256"):
+        o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES[tile_name], causal=causal, dtype=dtype, splits=splits)
+        o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
+        assert max_abs(o, o_ref) <= ATOL[dtype], tile_name
+        assert max_abs(lse, lse_ref) <= 1e-3, tile_name
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])

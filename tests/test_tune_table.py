@@ -34,7 +34,7 @@ def test_committed_table_names_only_built_tiles(fresh_table_cache):
     assert table["fa"] and table["gemm"], "tune_table.json is missing or empty"
     for key, entry in table["fa"].items():
         variant, dtype, D, _causal, _bh, _m, _n = _parse_fa_key(key)
-        tiles = {(c.block_m, c.block_n, c.waves) for c in cfgs.fa_candidates(variant, dtype, D)}
+        tiles = {(c.block_m, c.block_n, c.waves, c.stages) for c in cfgs.fa_candidates(variant, dtype, D)}
         assert tuple(entry["tile"]) in tiles, key
         timed = entry["timed"]
         best = "x".join(map(str, entry["tile"]))
@@ -52,7 +52,7 @@ def test_selection_returns_the_table_winner(fresh_table_cache):
         variant, dtype, D, causal, bh, m, n = _parse_fa_key(key)
         cands = cfgs.fa_candidates(variant, dtype, D)
         got = cfgs.choose_fa_tile(variant, dtype, D, causal, 1, bh, m, n, cands)
-        assert [got.block_m, got.block_n, got.waves] == entry["tile"], key
+        assert [got.block_m, got.block_n, got.waves, got.stages] == entry["tile"], key
     for key, entry in table["gemm"].items():
         M, N, K = (int(p[1:]) for p in key.split("|"))
         try:
@@ -113,5 +113,5 @@ def test_live_sweep_writes_selectable_entries(gpu, tmp_path, monkeypatch, fresh_
     for key, entry in table["fa"].items():
         variant, dtype, D, causal, bh, m, n = _parse_fa_key(key)
         got = cfgs.choose_fa_tile(variant, dtype, D, causal, 1, bh, m, n, cfgs.fa_candidates(variant, dtype, D))
-        assert [got.block_m, got.block_n, got.waves] == entry["tile"]
+        assert [got.block_m, got.block_n, got.waves, got.stages] == entry["tile"]
     assert list(cfgs.choose_gemm_tile(256, 256, 256)[:4]) == table["gemm"][cfgs.gemm_table_key(256, 256, 256)]["tile"]
