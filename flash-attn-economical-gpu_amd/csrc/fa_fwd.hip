@@ -290,7 +290,9 @@ struct FwdKernel {
   static constexpr int NVB = KC * DTL;
   static constexpr int KT_ELEMS = NKB * 512;  // 16-bit elements per K tile
   static constexpr int VT_ELEMS = NVB * 512;
-  static constexpr int RING = (WAVES >= 8) ? 3 : 2;  // tiles of K (and of V) resident in LDS
+  // Tiles of K (and of V) resident in LDS: 3 when one workgroup owns the CU, 2 when two
+  // four-wave workgroups share it (RT = 1: two waves per SIMD).
+  static constexpr int RING = (WAVES >= 8 || RT >= 2) ? 3 : 2;
   static constexpr int NKW = NKB / WAVES;            // DMA blocks per wave per K tile
   static constexpr int NVW = NVB / WAVES;
   static_assert(STAGES != 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
