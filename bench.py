@@ -137,6 +137,64 @@ def _traffic_probe(torch, flash_atten, tuner, mma, dev) -> int:
     return 0
 
 
+TRAFFIC_COMMAND = (
+    "export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/traffic -o fetch -- "
+    "python -u bench.py --traffic-probe && rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/traffic "
+    "-o write -- python -u bench.py --traffic-probe && python bench.py --traffic-summarize "
+    "gpurun_out/traffic/fetch_counter_collection.csv gpurun_out/traffic/write_counter_collection.csv"
+)
+
+
+def _traffic_summarize(fetch_csv: str, write_csv: str) -> int:
+    """Write TRAFFIC_FILE from the two counter passes over --traffic-probe. FETCH_SIZE and WRITE_SIZE
+    are KiB per dispatch (summed over the counter instances); each is scaled by the factor that
+    makes the calibration copy read/write exactly its 256 MiB."""
+    import csv
+
+    def per_dispatch(path: str) -> list[tuple[str, float]]:
+        acc: dict[int, list] = {}
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                d = int(r["Dispatch_Id"])
+                acc.setdefault(d, [r["Kernel_Name"], 0.0])[1] += float(r["Counter_Value"])
+        return [tuple(acc[d]) for d in sorted(acc)]
+
+    fetch, write = per_dispatch(fetch_csv), per_dispatch(write_csv)
+
+    def pick(rows, needle):
+        hits = [v for name, v in rows if needle in name]
+        if not hits:
+            raise SystemExit(f"no dispatch matching {needle!r}")
+        return hits[-1]
+
+    copy_bytes = 64 * 1024 * 1024 * 4
+    f_copy = next(v for name, v in fetch if "fa_fwd" not in name and "gemm" not in name)
+    w_copy = next(v for name, v in write if "fa_fwd" not in name and "gemm" not in name)
+    f_factor = round(copy_bytes / (f_copy * 1024), 2)
+    w_factor = round(copy_bytes / (w_copy * 1024), 2)
+    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
+    M, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
+    out = {
+        "command": TRAFFIC_COMMAND,
+        "note": ("Two counter passes over `bench.py --traffic-probe`: one 256 MiB fp32 copy (calibration), one "
+                 "attention forward (optimized variant through the tuner, fp16 B=4 H=32 N=8192 D=128 non-causal), "
+                 "one fp16 GEMM 8192^3 (tile from the tuning table). Counter values are KiB per dispatch; bytes = "
+                 "value x 1024 x factor."),
+        "calibration": {"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes, "FETCH_SIZE_KiB": f_copy,
+                        "WRITE_SIZE_KiB": w_copy, "fetch_factor": f_factor, "write_factor": w_factor},
+    }
+    for key, needle, algo in (("fa_fwd_b4h32n8192d128_f16", "fa_fwd", 4 * B * H * N * D * 2),
+                              ("gemm_f16_8192cube", "gemm", 2 * (M * K + K * Ng + M * Ng))):
+        fk, wk = pick(fetch, needle), pick(write, needle)
+        rd, wr = int(fk * 1024 * f_factor), int(wk * 1024 * w_factor)
+        out[key] = {"FETCH_SIZE_KiB": fk, "WRITE_SIZE_KiB": wk, "bytes_read": rd, "bytes_written": wr,
+                    "bytes_per_launch": rd + wr, "algorithmic_bytes_per_launch": algo,
+                    "ratio_to_algorithmic": round((rd + wr) / algo, 4)}
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=2) + "\n")
+    print(json.dumps(out, indent=2))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,7 +206,11 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one 256 MiB copy (counter calibration), one attention forward and one GEMM, then exit "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
+    ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn the two counter passes into the HBM traffic table read by the bench line")
     args = ap.parse_args()
+    if args.traffic_summarize:
+        return _traffic_summarize(*args.traffic_summarize)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
