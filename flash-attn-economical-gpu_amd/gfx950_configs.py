@@ -63,8 +63,8 @@ STAGES_BY_VARIANT = {
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).
 GEMM_TILE_SPACE = [
-    (256, 256, 64, 4),
     (256, 256, 64, 8),
+    (256, 256, 64, 4),
     (256, 256, 32, 8),
     (256, 128, 64, 8),
     (128, 256, 64, 8),
@@ -235,9 +235,12 @@ def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None =
             "(M % 64 == 0 and N % 256 == 0), with K % 32 == 0"
         )
     if hint is not None:
-        for t in cands:
-            if t[:3] == tuple(hint):
-                return (*t, _gemm_group_m(M, N, K, t))
+        # (block_m, block_n, block_k[, waves]) hints narrow the candidates; the table still ranks them
+        hint = tuple(hint)
+        hinted = [t for t in cands if t[:len(hint)] == hint]
+        if not hinted and len(hint) > 3:  # no built tile with that wave count: keep the sizes
+            hinted = [t for t in cands if t[:3] == hint[:3]]
+        cands = hinted or cands
     entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
     if entry is not None:
         for t in cands:

@@ -70,6 +70,8 @@ class _HipMatmulKernel:
         hint = None
         if all(kwargs.get(key) is not None for key in ("BLOCK_M", "BLOCK_N", "BLOCK_K")):
             hint = (int(kwargs["BLOCK_M"]), int(kwargs["BLOCK_N"]), int(kwargs["BLOCK_K"]))
+            if kwargs.get("num_warps") is not None:
+                hint = (*hint, int(kwargs["num_warps"]))
         tile = _gemm_tile(M, N, K, hint, kwargs.get("GROUP_M"))
         hip_lib.gemm_f16(a, b, c, tile)
 

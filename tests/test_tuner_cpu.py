@@ -272,6 +272,18 @@ def test_gemm_selector_prefers_large_tiles_and_hints():
     assert mma._select_2d_contiguous_config(8192, 8192, 8192)[:3] in [(256, 256, 64), (256, 256, 32),
                                                                      (256, 128, 64), (128, 256, 64)]
     assert cfgs.choose_gemm_tile(1024, 1024, 256, hint=(128, 128, 64))[:3] == (128, 128, 64)
+    # block sizes + wave count narrow the candidates; a wave count that is not built keeps the sizes
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192, hint=(256, 256, 64, 4))[:4] == (256, 256, 64, 4)
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192, hint=(256, 256, 64, 8))[:4] == (256, 256, 64, 8)
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192, hint=(256, 256, 64, 2))[:3] == (256, 256, 64)
+
+
+def test_gemm_launch_hints_keep_the_tuned_tile():
+    """BLOCK_* hints equal to the tuned tile's sizes (what _select_2d_contiguous_config returns and
+    test_mma.py passes back) must launch the tuned tile, wave count included."""
+    bm, bn, bk, group_m, warps, _ = mma._select_2d_contiguous_config(8192, 8192, 8192)
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192, hint=(bm, bn, bk))[:4] == (bm, bn, bk, warps)
+    assert cfgs.choose_gemm_tile(8192, 8192, 8192, hint=(bm, bn, bk, warps))[:4] == (bm, bn, bk, warps)
 
 
 def test_cache_eviction_hint_false_without_gpu():
