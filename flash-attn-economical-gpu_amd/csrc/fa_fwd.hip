@@ -16,18 +16,22 @@
 //    gfx950 transposing read ds_read_b64_tr_b16: in a 16-lane group, result lane i element c is
 //    element (i & 3) of the 8-byte chunk addressed by group lane 4c + (i >> 2). Each lane of group
 //    lane L addresses key J + (L >> 2), columns d0 + 4 (L & 3); lane i then holds V[J + c][d0 + i].
-//  * K and V tiles are staged HBM -> registers -> LDS with precomputed per-thread addresses; the
-//    next tile's global loads are issued before the current tile is computed.
-//  * stages=1 (basic): one LDS buffer, two barriers per tile.
-//    stages=2 (optimized / sliced): K/V double-buffered in LDS, one barrier per tile.
+//  * stages=1 (basic) and stages=2: K and V tiles are staged HBM -> registers -> LDS with
+//    precomputed per-thread addresses (padded rows), the next tile's global loads issued before the
+//    current tile is computed; stages=1 keeps one LDS buffer (two barriers per tile), stages=2
+//    double-buffers K/V (one barrier per tile).
+//    stages=3: software pipeline inside each wave (QK MFMAs of tile u+1 interleaved with the
+//    softmax VALU work of tile u, PV of tile u with the row max of tile u+1), K/V brought into a
+//    ring of fragment-major LDS tiles by LDS-DMA loads (see the stages=3 branch of run()).
 //    LDS fragment reads are issued a few MFMAs ahead of use (scheduling-group hints).
 //  * Softmax in the exp2 domain with scale*log2(e) folded into one FMA per score; the O rescale is
 //    lazy: the exponent offset only moves when a row max grows by more than 8 (log2 units), so
-//    P <= 256 and the 4*D accumulator multiplies run on a handful of tiles per row. The row sum is
-//    accumulated from the rounded P (v_dot2 with (1, 1)), i.e. the same P the PV product uses.
+//    P <= 256 and the 4*D accumulator multiplies run on a handful of tiles per row. For fp16 the
+//    row sum is accumulated from the rounded P (v_dot2 with (1, 1)), i.e. the same P the PV
+//    product uses; for bf16 from the fp32 values.
 //  * Causal (top-left, row i sees keys j <= i as flash_atten.py:103-105) skips KV tiles past the
-//    diagonal and waves whose rows all precede a tile, masks only diagonal tiles, and walks query
-//    blocks heaviest-first.
+//    diagonal (stages 1/2 also skip waves whose rows all precede a tile), masks only diagonal
+//    tiles, and walks query blocks heaviest-first.
 //  * GQA: query head h reads KV head h / (H / H_kv); no K/V expansion.
 //  * Split-KV: the SPLIT instantiation writes fp32 normalised partial O and partial LSE per KV
 //    split; fa_merge_kernel combines them: lse = ln sum_j exp(lse_j), O = sum_j exp(lse_j - lse) O_j.
