@@ -122,6 +122,13 @@ int64_t fa_fwd_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t D, int32
   return lse_off + rows * 4;
 }
 
+int32_t fa_fwd_pack_group(int32_t H, int32_t H_kv, int32_t M, int32_t causal, int32_t block_m, int32_t splits) {
+  if (H <= 0 || H_kv <= 0 || H % H_kv != 0 || M <= 0 || block_m <= 0) return 1;
+  const int32_t group = H / H_kv;
+  if (splits <= 1 || causal || group <= 1 || (int64_t)M * group > block_m) return 1;
+  return group;
+}
+
 int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile) {
   bool split = false;
   int code = FA_OK;
@@ -155,10 +162,15 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
 
   const int bm = a->tile.block_m, bn = a->tile.block_n;
   const int splits = a->tile.splits < 1 ? 1 : a->tile.splits;
-  const int64_t m_blocks = (a->M + bm - 1) / bm;
+  // Decode shapes: when every query row of a GQA group fits in one tile (non-causal), the group's
+  // query heads share the tile's rows, so each workgroup reads its kv head's K/V once for all of
+  // them instead of once per query head.
+  const int group = a->H / a->H_kv;
+  const int pack = fa_fwd_pack_group(a->H, a->H_kv, a->M, a->causal, bm, splits);
+  const int64_t m_blocks = ((int64_t)a->M * pack + bm - 1) / bm;
   const int64_t n_tiles = a->N > 0 ? (a->N + bn - 1) / bn : 1;
   const int64_t tiles_per_split = (n_tiles + splits - 1) / splits;
-  const int64_t total = m_blocks * a->B * a->H * splits;
+  const int64_t total = m_blocks * a->B * (pack > 1 ? a->H_kv : a->H) * splits;
   if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large (%lld workgroups)", (long long)total);
 
   fa::FwdParams p;
@@ -174,7 +186,8 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
   p.so0 = a->o_stride[0]; p.so1 = a->o_stride[1]; p.so2 = a->o_stride[2];
   p.sl0 = a->lse_stride[0]; p.sl1 = a->lse_stride[1]; p.sl2 = a->lse_stride[2];
   p.B = a->B; p.H = a->H; p.Hkv = a->H_kv; p.M = a->M; p.N = a->N;
-  p.group = a->H / a->H_kv;
+  p.group = group;
+  p.pack = pack;
   p.sm_scale = a->sm_scale;
   p.c = a->sm_scale * 1.4426950408889634f;
   p.causal = a->causal ? 1 : 0;

@@ -360,19 +360,32 @@ struct FwdKernel {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, col = lane & 31, hh = lane >> 5;
 
-    // Logical block id: XCD-local, then (bh, split, m-block) with the m-block fastest.
+    // Logical block id: XCD-local, then (bh, split, m-block) with the m-block fastest. bh is
+    // (batch, query head), or (batch, kv head) when the query heads of a GQA group are packed
+    // into the rows (pack > 1, decode shapes): row r is then query head h + r / M, position r % M.
     const int pid = xcd_remap(blockIdx.x, p.total_blocks);
     int mb = pid % p.m_blocks;
     const int rest = pid / p.m_blocks;
     const int split = rest % p.splits;
     const int bh = rest / p.splits;
     if (p.causal) mb = p.m_blocks - 1 - mb;  // heaviest query blocks first
-    const int b = bh / p.H, h = bh % p.H;
-    const int hk = h / p.group;
+    int b, h, hk;
+    if (p.pack > 1) {
+      b = bh / p.Hkv;
+      hk = bh % p.Hkv;
+      h = hk * p.group;
+    } else {
+      b = bh / p.H;
+      h = bh % p.H;
+      hk = h / p.group;
+    }
+    const int rows = p.M * p.pack;       // query rows of this workgroup's row space
     const int m0 = mb * BM;
     const int wrow0 = m0 + wave * ROWS;  // first query row of this wave
+    const bool wave_has_rows = wrow0 < rows;
+    auto row_head = [&](int r) { return p.pack > 1 ? h + r / p.M : h; };
+    auto row_pos = [&](int r) { return p.pack > 1 ? r % p.M : r; };
 
-    const uint16_t* qbase = p.q + (int64_t)b * p.sq0 + (int64_t)h * p.sq1;
     Ctx cx;
     cx.r0 = tid / CPR;
     cx.c8 = tid % CPR;
@@ -387,10 +400,12 @@ struct FwdKernel {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int row = wrow0 + rt * 32 + col;
+      const uint16_t* qrow =
+          p.q + (int64_t)b * p.sq0 + (int64_t)row_head(row) * p.sq1 + (int64_t)row_pos(row) * p.sq2;
 #pragma unroll
       for (int cc = 0; cc < DC; ++cc) {
         u32x4 val = {0u, 0u, 0u, 0u};
-        if (row < p.M) val = *reinterpret_cast<const u32x4*>(qbase + (int64_t)row * p.sq2 + cc * 16 + hh * 8);
+        if (row < rows) val = *reinterpret_cast<const u32x4*>(qrow + cc * 16 + hh * 8);
         qf[rt][cc] = val;
       }
     }
@@ -420,7 +435,9 @@ struct FwdKernel {
     const int g = lane & 15;
     const int lane_v_off = (4 * hh + (g >> 2)) * VSTR + 16 * ((lane >> 4) & 1) + 4 * (g & 3);
 
-    auto active = [&](int t) { return !(p.causal && t * BN > wrow0 + ROWS - 1); };
+    // Waves skip tiles they have no work in: rows past the row space (packed decode tiles), or
+    // (causal) rows that all precede the tile.
+    auto active = [&](int t) { return wave_has_rows && !(p.causal && t * BN > wrow0 + ROWS - 1); };
 
     if (STAGES == 1) {
       uint16_t* ks = smem;
@@ -508,9 +525,11 @@ struct FwdKernel {
           if (i + 1 < RING) issue_v(i);
         }
         wait_vm_lds_barrier<0>();
-        qk_fm(sa, qf, klane);
-        qk_schedule();
-        tile_max(sa, mxa);           // masks, if tile 0 needs them, come in step 0
+        if (wave_has_rows) {
+          qk_fm(sa, qf, klane);
+          qk_schedule();
+          tile_max(sa, mxa);         // masks, if tile 0 needs them, come in step 0
+        }
         wait_vm_lds_barrier<0>();    // every wave is done with K slot 0 before step 0 refills it
       }
       // Masks for tile u (rare: sequence end, causal diagonal) and the row max they change. The
@@ -527,15 +546,17 @@ struct FwdKernel {
       auto step = [&](STile& cur, float (&mx_cur)[RT], STile& nxt, float (&mx_nxt)[RT], int u) {
         issue_k(u + RING);      // into K_u's slot (read in step u-1)
         issue_v(u + RING - 1);  // into V_{u-1}'s slot (read in step u-1)
-        fix_masked(cur, mx_cur, u);
-        rescale(mx_cur, acc, m_use, l_i, p.c);
-        u32x4 pk[KC][RT];
-        exp_pack(cur, pk, m_use, l_i, p.c);
-        qk_fm(nxt, qf, klane + ((u + 1) % RING) * KT_ELEMS);
-        x_schedule();
-        pv_fm(acc, pk, vlane + (u % RING) * VT_ELEMS);
-        tile_max(nxt, mx_nxt);
-        y_schedule();
+        if (wave_has_rows) {    // waves without rows still move their share of K/V
+          fix_masked(cur, mx_cur, u);
+          rescale(mx_cur, acc, m_use, l_i, p.c);
+          u32x4 pk[KC][RT];
+          exp_pack(cur, pk, m_use, l_i, p.c);
+          qk_fm(nxt, qf, klane + ((u + 1) % RING) * KT_ELEMS);
+          x_schedule();
+          pv_fm(acc, pk, vlane + (u % RING) * VT_ELEMS);
+          tile_max(nxt, mx_nxt);
+          y_schedule();
+        }
         // Step u+1 reads K_{u+2} and V_{u+1}. With RING = 3 they were issued in step u-1 (or
         // before the loop), and this step's loads may stay in flight.
         if (RING > 2 && u + RING < ntiles)
@@ -545,6 +566,7 @@ struct FwdKernel {
       };
       // The last tile: no successor to overlap with.
       auto last = [&](STile& cur, float (&mx_cur)[RT], int u) {
+        if (!wave_has_rows) return;
         fix_masked(cur, mx_cur, u);
         rescale(mx_cur, acc, m_use, l_i, p.c);
         u32x4 pk[KC][RT];
@@ -610,9 +632,11 @@ struct FwdKernel {
       const int i = wrow0 + rt * 32 + col;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       const float lse_val = (l > 0.f) ? (m_use[rt] * p.c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
-      if (i < p.M) {
+      if (i < rows) {
+        const int hr = row_head(i), mr = row_pos(i);
         if (SPLIT) {
-          float* wo = p.ws_o + ((int64_t)(split * p.B * p.H + bh) * p.M + i) * D;
+          const int64_t wrow = (int64_t)(split * p.B + b) * p.H + hr;  // [split][b][h][m] rows
+          float* wo = p.ws_o + (wrow * p.M + mr) * D;
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt)
 #pragma unroll
@@ -621,9 +645,9 @@ struct FwdKernel {
                              acc[dt][rt][4 * gq + 2] * inv, acc[dt][rt][4 * gq + 3] * inv};
               *reinterpret_cast<floatx4*>(wo + dt * 32 + 8 * gq + 4 * hh) = val;
             }
-          if (hh == 0) p.ws_lse[(int64_t)(split * p.B * p.H + bh) * p.M + i] = lse_val;
+          if (hh == 0) p.ws_lse[wrow * p.M + mr] = lse_val;
         } else {
-          uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)h * p.so1 + (int64_t)i * p.so2;
+          uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)hr * p.so1 + (int64_t)mr * p.so2;
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt)
 #pragma unroll
@@ -633,7 +657,7 @@ struct FwdKernel {
               *reinterpret_cast<u32x2*>(orow + dt * 32 + 8 * gq + 4 * hh) = val;
             }
           if (p.lse != nullptr && hh == 0)
-            p.lse[(int64_t)b * p.sl0 + (int64_t)h * p.sl1 + (int64_t)i * p.sl2] = lse_val;
+            p.lse[(int64_t)b * p.sl0 + (int64_t)hr * p.sl1 + (int64_t)mr * p.sl2] = lse_val;
         }
       }
     }

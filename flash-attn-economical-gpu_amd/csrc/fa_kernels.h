@@ -22,6 +22,8 @@ struct FwdParams {
   int64_t sl0, sl1, sl2;
   int32_t B, H, Hkv, M, N;
   int32_t group;            // H / Hkv
+  int32_t pack;             // 1, or group: the query heads of a kv head share one row space
+                            // (row r = head offset r / M, position r % M); grid over (b, kv head)
   float c;                  // sm_scale * log2(e): exp(x*sm_scale) == exp2(x*c)
   float sm_scale;
   int32_t causal;

@@ -119,7 +119,9 @@ class _HipAttentionKernel:
         B = q.shape[0]
         tile = _tile_for(self.variant, q.dtype, D, causal, B, H, M, N, kwargs)
         splits = kwargs.get("SPLITS")
-        splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n) if splits is None else int(splits)
+        if splits is None:
+            splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n, H_kv=k.shape[1], causal=causal)
+        splits = int(splits)
         workspace = kwargs.get("workspace")
         need = hip_lib.workspace_bytes(B, H, M, D, splits)
         if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
@@ -207,7 +209,8 @@ def sdpa(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, is_caus
     splits = 1
     workspace = None
     if variant_code == hip_lib.FA_VARIANT_SLICED:
-        splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n)
+        splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n, H_kv=key.shape[1],
+                                    causal=bool(is_causal))
         need = hip_lib.workspace_bytes(B, H, M, D, splits)
         if need:
             workspace = torch.empty(need, dtype=torch.uint8, device=query.device)

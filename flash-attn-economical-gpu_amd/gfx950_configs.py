@@ -208,15 +208,27 @@ def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M:
     return candidates[0]
 
 
-def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int) -> int:
+def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int, H_kv: int | None = None,
+                  causal: bool = False) -> int:
     """KV splits for the sliced variant: split until ~TARGET_WORKGROUPS workgroups are in flight,
-    keeping at least two KV tiles per split."""
-    base = max(1, math.ceil(M / block_m) * B * H)
+    keeping at least two KV tiles per split. Split launches of decode shapes pack the query heads
+    of a GQA group into one tile (hip_lib.pack_group), so they count workgroups per kv head."""
     n_tiles = max(1, math.ceil(N / block_n))
-    if base >= TARGET_WORKGROUPS or n_tiles < 4:
+    if n_tiles < 4:
         return 1
-    splits = min(math.ceil(TARGET_WORKGROUPS / base), n_tiles // 2, MAX_SPLITS)
-    return max(1, splits)
+
+    def splits_for(base: int) -> int:
+        if base >= TARGET_WORKGROUPS:
+            return 1
+        return max(1, min(math.ceil(TARGET_WORKGROUPS / base), n_tiles // 2, MAX_SPLITS))
+
+    H_kv = H if H_kv is None else H_kv
+    group = hip_lib.pack_group(H, H_kv, M, causal, block_m, 2)
+    if group > 1:
+        packed = splits_for(max(1, math.ceil(M * group / block_m) * B * H_kv))
+        if packed > 1:
+            return packed
+    return splits_for(max(1, math.ceil(M / block_m) * B * H))
 
 
 def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None = None) -> tuple[int, int, int, int, int]:

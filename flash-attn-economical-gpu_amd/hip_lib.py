@@ -17,7 +17,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libfa_gfx950.so"
 RESOURCES_PATH = HERE / "kernel_resources.json"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FA_OK, FA_EINVAL, FA_ENOTSUP, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
 FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1
@@ -108,6 +108,7 @@ SIGNATURES = {
         ctypes.c_int64,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
     ),
+    "fa_fwd_pack_group": (ctypes.c_int32, [ctypes.c_int32] * 6),
     "fa_fwd_supported": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(FaTile)]),
     "gemm_f16": (
         ctypes.c_int,
@@ -204,6 +205,11 @@ def make_tile(block_m: int, block_n: int, waves: int, stages: int, splits: int =
 
 def workspace_bytes(B: int, H: int, M: int, D: int, splits: int) -> int:
     return int(load().fa_fwd_workspace_bytes(B, H, M, D, splits))
+
+
+def pack_group(H: int, H_kv: int, M: int, causal: bool, block_m: int, splits: int) -> int:
+    """Query heads fa_fwd packs into one tile's rows (1 = none); see fa_fwd_pack_group."""
+    return int(load().fa_fwd_pack_group(H, H_kv, M, int(bool(causal)), block_m, splits))
 
 
 def fa_fwd_supported(variant: int, dtype: torch.dtype, D: int, tile: FaTile) -> bool:

@@ -522,7 +522,7 @@ class FlashAttentionBlockDNomaskTuner(FlashAttentionTuner):
             config["BLOCK_DMODEL"] = int(self.tune_args.BLOCK_DMODEL or self.D)
             config["BLOCK_DMODEL_OUTER"] = int(self.tune_args.BLOCK_DMODEL_OUTER or self.D)
             config["splits"] = cfgs.choose_splits(self.B, self.H, self.M, self.N, int(config["BLOCK_M"]),
-                                                  int(config["BLOCK_N"]))
+                                                  int(config["BLOCK_N"]), H_kv=self.H_kv, causal=self.causal)
         return out
 
     def _build_candidate_launch(

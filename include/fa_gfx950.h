@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 enum {
   FA_OK = 0,
@@ -125,6 +125,13 @@ int fa_fwd(const fa_fwd_args* args, void* stream);
 
 /* Bytes of split-KV workspace fa_fwd needs for these sizes (0 when splits <= 1). */
 int64_t fa_fwd_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t D, int32_t splits);
+
+/* Query heads that fa_fwd packs into one tile's rows (1 = none): decode-shaped split-KV launches
+ * (splits > 1, non-causal, H > H_kv, M * H / H_kv <= block_m) give each workgroup all query heads
+ * of one kv head, so K/V are read once per kv head; the grid then runs over (batch, kv head).
+ * Callers sizing `splits` for a target grid use it to count workgroups. Part of the behaviour of
+ * the sliced path (flash_atten.py:261-361 re-defined as split-KV), no separate reference entry. */
+int32_t fa_fwd_pack_group(int32_t H, int32_t H_kv, int32_t M, int32_t causal, int32_t block_m, int32_t splits);
 
 /* Is this (variant, dtype, D, tile) built? Returns FA_OK or FA_ENOTSUP. */
 int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile);

@@ -1,0 +1,104 @@
+"""Decode-shaped split-KV (small M, long N): the sliced variant with KV splits, where the query
+heads of a GQA group are packed into one tile's rows (fa_fwd_pack_group) so K/V are read once per
+kv head. Parity against the exact oracle, as the other C-ABI tests."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flash_atten
+import gfx950_configs as cfgs
+import hip_lib
+import oracle
+from helpers import ATOL, make_qkv, max_abs, to_device
+
+F16, BF16 = torch.float16, torch.bfloat16
+SLICED = hip_lib.FA_VARIANT_SLICED
+
+
+def test_pack_rule():
+    # packs only split launches, non-causal, grouped, when the whole group fits one tile
+    assert hip_lib.pack_group(32, 8, 1, False, 128, 16) == 4
+    assert hip_lib.pack_group(32, 8, 32, False, 128, 16) == 4
+    assert hip_lib.pack_group(32, 8, 33, False, 128, 16) == 1
+    assert hip_lib.pack_group(32, 8, 1, True, 128, 16) == 1
+    assert hip_lib.pack_group(32, 8, 1, False, 128, 1) == 1
+    assert hip_lib.pack_group(32, 32, 1, False, 128, 16) == 1
+    assert hip_lib.pack_group(12, 2, 1, False, 128, 16) == 6
+    # the split count then targets the packed grid: one workgroup per (batch, kv head, split)
+    s = cfgs.choose_splits(1, 32, 1, 32768, 128, 64, H_kv=8)
+    assert s == cfgs.MAX_SPLITS
+    assert cfgs.choose_splits(1, 32, 1, 32768, 128, 64, H_kv=32) < s
+
+
+def _run(q, k, v, *, dtype, tile, splits, causal=False, lse=True):
+    dev = "cuda:0"
+    qd, kd, vd = (to_device(x, dtype, dev) for x in (q, k, v))
+    B, H, M, D = qd.shape
+    o = torch.empty_like(qd)
+    l = torch.empty((B, H, M), dtype=torch.float32, device=dev) if lse else None
+    nbytes = hip_lib.workspace_bytes(B, H, M, D, splits)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+    bm, bn, waves, stages = tile
+    hip_lib.fa_fwd(qd, kd, vd, o, l, sm_scale=D ** -0.5, causal=causal, variant=SLICED,
+                   tile=hip_lib.make_tile(bm, bn, waves, stages, splits), workspace=ws)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), (l.cpu().numpy() if lse else None)
+
+
+DECODE = [
+    # name, B, H, Hkv, M, N, D, dtype, tile (bm, bn, waves, stages), splits
+    ("llama_m1", 2, 32, 8, 1, 2000, 128, F16, (128, 64, 4, 3), 16),
+    ("llama_m4_bf16", 1, 32, 8, 4, 1500, 128, BF16, (128, 64, 4, 3), 8),
+    ("qwen_m1", 1, 12, 2, 1, 4096, 128, BF16, (128, 64, 4, 3), 32),
+    ("qwen_m7_ragged", 1, 12, 2, 7, 777, 128, F16, (128, 64, 4, 3), 5),
+    ("g8_d64", 3, 8, 1, 3, 1000, 64, F16, (128, 64, 4, 3), 6),
+    ("w8_tile", 1, 16, 2, 9, 900, 128, BF16, (256, 64, 8, 3), 4),
+    ("double_buffered", 2, 32, 8, 2, 1200, 128, F16, (128, 64, 4, 2), 8),
+    ("group_exceeds_tile", 1, 16, 1, 9, 640, 64, F16, (128, 64, 4, 3), 4),  # 16*9 > 128: no packing
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", DECODE, ids=[c[0] for c in DECODE])
+def test_decode_split_kv_parity(gpu, case):
+    name, B, H, Hkv, M, N, D, dtype, tile, splits = case
+    print(f"[decode] {name} B={B} H={H} Hkv={Hkv} M={M} N={N} D={D} {dtype} tile={tile} splits={splits} "
+          f"pack={hip_lib.pack_group(H, Hkv, M, False, tile[0], splits)}", flush=True)
+    q, k, v = make_qkv(4000 + len(name), B, H, Hkv, M, N, D, dtype)
+    o, lse = _run(q, k, v, dtype=dtype, tile=tile, splits=splits)
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=False)
+    assert np.isfinite(o).all()
+    assert max_abs(o, o_ref) <= ATOL[dtype]
+    assert max_abs(lse, lse_ref) <= 1e-3
+
+
+@pytest.mark.gpu
+def test_decode_packed_equals_unpacked(gpu):
+    """Packing changes which workgroup computes a row; it matches the same split launch with one
+    query head per kv head (H_kv = H, K/V expanded) up to the rounding of P (the lazy-rescale
+    offset is decided per wave, and a wave now holds rows of several heads)."""
+    B, H, Hkv, M, N, D = 1, 32, 8, 2, 3000, 128
+    print("[decode] packed vs expanded", flush=True)
+    q, k, v = make_qkv(4242, B, H, Hkv, M, N, D, F16)
+    ke, ve = (np.repeat(x, H // Hkv, axis=1) for x in (k, v))
+    o1, l1 = _run(q, k, v, dtype=F16, tile=(128, 64, 4, 3), splits=16)
+    o2, l2 = _run(q, ke, ve, dtype=F16, tile=(128, 64, 4, 3), splits=16)
+    assert hip_lib.pack_group(H, Hkv, M, False, 128, 16) == 4 and hip_lib.pack_group(H, H, M, False, 128, 16) == 1
+    assert max_abs(o1, o2) <= 2e-3
+    assert max_abs(l1, l2) <= 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 3])
+def test_decode_through_sdpa_entry(gpu, M):
+    """flash_atten.sdpa (sliced) picks the split count and packing itself."""
+    B, H, Hkv, N, D = 2, 12, 2, 5000, 128
+    print(f"[decode] sdpa entry M={M}", flush=True)
+    q, k, v = make_qkv(77 + M, B, H, Hkv, M, N, D, BF16)
+    qd, kd, vd = (to_device(x, BF16, "cuda:0") for x in (q, k, v))
+    out = flash_atten.sdpa(qd, kd, vd, is_causal=False, scale=D ** -0.5, variant="sliced")
+    torch.cuda.synchronize()
+    o_ref, _ = oracle.attention(q, k, v, causal=False)
+    assert max_abs(out.float().cpu().numpy(), o_ref) <= ATOL[BF16]
