@@ -28,14 +28,17 @@ import hip_lib
 VARIANTS = {"basic": hip_lib.FA_VARIANT_BASIC, "optimized": hip_lib.FA_VARIANT_OPT,
             "sliced": hip_lib.FA_VARIANT_SLICED}
 
-# (name, dtype, B, H, H_kv, N, D, causal, variants) -- the BASELINE.json configurations
+# (name, dtype, B, H, H_kv, M, N, D, causal, variants) -- the BASELINE.json configurations, plus
+# decode shapes (a few query rows against a long KV cache) for the sliced variant
 FA_SWEEP = (
-    [("fp16_d128", torch.float16, 4, 32, 32, n, 128, c, ("basic", "optimized", "sliced"))
+    [("fp16_d128", torch.float16, 4, 32, 32, n, n, 128, c, ("basic", "optimized", "sliced"))
      for n in (1024, 2048, 4096, 8192, 16384) for c in (False, True)]
-    + [("bf16_d256", torch.bfloat16, 2, 16, 16, n, 256, False, ("basic", "optimized", "sliced"))
+    + [("bf16_d256", torch.bfloat16, 2, 16, 16, n, n, 256, False, ("basic", "optimized", "sliced"))
        for n in (1024, 2048, 4096, 8192)]
-    + [("fp16_d64_cfg1", torch.float16, 1, 4, 4, 512, 64, False, ("basic", "optimized", "sliced"))]
-    + [("ttft_bf16_gqa", torch.bfloat16, 1, 12, 2, n, 128, True, ("sliced", "optimized")) for n in (4096, 16384)]
+    + [("fp16_d64_cfg1", torch.float16, 1, 4, 4, 512, 512, 64, False, ("basic", "optimized", "sliced"))]
+    + [("ttft_bf16_gqa", torch.bfloat16, 1, 12, 2, n, n, 128, True, ("sliced", "optimized")) for n in (4096, 16384)]
+    + [("decode_bf16_gqa", torch.bfloat16, b, 32, 8, 1, n, 128, False, ("sliced",))
+       for b, n in ((1, 8192), (1, 32768), (1, 131072), (8, 32768), (32, 8192))]
 )
 GEMM_SWEEP = [(n, n, n) for n in (1024, 2048, 4096, 8192, 16384)] + [(8192, 8192, 256), (1024, 1024, 256)]
 GROUP_MS = (4, 8, 16)
@@ -58,12 +61,12 @@ def _time(fn, warmup: int, iters: int) -> float:
 
 def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5, log=print) -> None:
     dev = torch.device("cuda:0")
-    for name, dtype, B, H, Hkv, N, D, causal, variants in sweep:
-        q = torch.randn(B, H, N, D, device=dev, dtype=dtype)
+    for name, dtype, B, H, Hkv, M, N, D, causal, variants in sweep:
+        q = torch.randn(B, H, M, D, device=dev, dtype=dtype)
         k = torch.randn(B, Hkv, N, D, device=dev, dtype=dtype)
         v = torch.randn(B, Hkv, N, D, device=dev, dtype=dtype)
         o = torch.empty_like(q)
-        flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
+        flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal and M == N else M * N)
         for vname in variants:
             variant = VARIANTS[vname]
             results = {}
@@ -71,22 +74,22 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
                 splits = 1
                 ws = None
                 if variant == hip_lib.FA_VARIANT_SLICED:
-                    splits = cfgs.choose_splits(B, H, N, N, cand.block_m, cand.block_n, H_kv=Hkv, causal=causal)
-                    need = hip_lib.workspace_bytes(B, H, N, D, splits)
+                    splits = cfgs.choose_splits(B, H, M, N, cand.block_m, cand.block_n, H_kv=Hkv, causal=causal)
+                    need = hip_lib.workspace_bytes(B, H, M, D, splits)
                     ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
                 tile = cfgs.FaTileChoice(cand.block_m, cand.block_n, cand.waves, cand.stages, splits).to_c()
                 ms = _time(lambda: hip_lib.fa_fwd(q, k, v, o, None, sm_scale=D ** -0.5, causal=causal,
                                                   variant=variant, tile=tile, workspace=ws), warmup, iters)
                 results[f"{cand.block_m}x{cand.block_n}x{cand.waves}x{cand.stages}"] = round(ms, 4)
             best = min(results, key=results.get)
-            key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, N, N)
+            key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, M, N)
             table["fa"][key] = {
                 "tile": [int(x) for x in best.split("x")],
                 "ms": results[best],
                 "tflops": round(flops / results[best] / 1e9, 1),
                 "timed": results,
             }
-            log(f"[tune] attention {name} N={N} causal={causal} {vname}: best {best} "
+            log(f"[tune] attention {name} B={B} M={M} N={N} causal={causal} {vname}: best {best} "
                 f"{results[best]:.3f} ms ({flops / results[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
         del q, k, v, o
         torch.cuda.empty_cache()

@@ -103,7 +103,7 @@ def test_sliced_candidates_have_split_kernels():
 def test_live_sweep_writes_selectable_entries(gpu, tmp_path, monkeypatch, fresh_table_cache):
     print("[tune] live sweep: fp16 D=64 B1 H4 N=512, gemm 256x256x256", flush=True)
     table = {"fa": {}, "gemm": {}}
-    sweep = [("t", torch.float16, 1, 4, 4, 512, 64, False, ("basic", "sliced"))]
+    sweep = [("t", torch.float16, 1, 4, 4, 512, 512, 64, False, ("basic", "sliced"))]
     gfx950_tune.tune_attention(table, sweep=sweep, warmup=1, iters=2, log=lambda m: None)
     gfx950_tune.tune_gemm(table, sweep=[(256, 256, 256)], warmup=1, iters=2, log=lambda m: None)
     assert len(table["fa"]) == 2 and len(table["gemm"]) == 1
