@@ -63,7 +63,7 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 }
 
 // Pipeline of a launch: basic keeps one K/V buffer (1); optimized and sliced double-buffer K/V (2),
-// or, when the tile asks for stages=3, also run the two wave groups half a tile apart (ping-pong).
+// or, when the tile asks for stages=3, run the software-pipelined kernel (LDS-DMA ring).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
   return (t != nullptr && t->stages == 3) ? 3 : 2;
@@ -273,6 +273,11 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
     return fail(FA_EINVAL, "leading dimensions lda=%lld ldb=%lld ldc=%lld invalid", (long long)lda,
                 (long long)ldb, (long long)ldc);
   if (tile->group_m < 1) return fail(FA_EINVAL, "group_m must be >= 1");
+  // The kernel addresses a tile's A rows and B columns (all of K) as raw buffers with 32-bit byte
+  // offsets.
+  if ((int64_t)e->block_m * lda * 2 > 0xffffffffLL || ((int64_t)(K - 1) * ldb + e->block_n) * 2 > 0xffffffffLL)
+    return fail(FA_ENOTSUP, "GEMM operand spans beyond 4 GiB per tile (lda=%lld ldb=%lld K=%d)", (long long)lda,
+                (long long)ldb, K);
   fa::GemmParams p;
   p.a = static_cast<const uint16_t*>(a);
   p.b = static_cast<const uint16_t*>(b);

@@ -7,15 +7,25 @@
 // gfx950 design:
 //  * v_mfma_f32_32x32x16_f16 computes C^T = B^T A^T per 32x32 tile, so the accumulator gives each
 //    lane four consecutive output columns of one row (8-byte stores).
-//  * A slabs are staged in LDS as [m][k] (16-byte skewed rows): the MFMA B operand (A^T columns) is
-//    one ds_read_b128 per lane.
-//  * B slabs are staged untransposed, [k][n] (64-byte skewed rows). The MFMA A operand (B^T rows,
-//    8 consecutive k per lane) comes from two ds_read_b64_tr_b16 transposing reads: in each 16-lane
-//    group, lane L addresses row k0 + (L >> 2) at columns n0 + 4 (L & 3), and result lane i then
-//    holds B[k0 + c][n0 + i] for c = 0..3. No register shuffles.
-//  * Each slab is loaded HBM -> registers while the previous one is multiplied; LDS is double
-//    buffered with one barrier per slab; LDS fragment reads for the next 16-deep chunk are issued
-//    while the current chunk's MFMAs run (scheduling-group hints).
+//  * K slabs (BK deep) reach LDS by LDS-DMA (buffer_load_dwordx4 ... lds), no staging registers,
+//    into a ring of RING slabs: slab s is requested RING-1 slabs before it is multiplied, and the
+//    barrier ending a slab waits only for the next slab's loads (vmcnt), not for the newer ones.
+//  * LDS slabs keep HBM's row-major order, so one DMA instruction (1 KiB, 16 bytes per lane) reads
+//    whole rows: 1024 / (2 BK) rows of A or 1024 / (2 BN) rows of B. Reads are made conflict-free by
+//    XOR-swizzling the 16-byte chunks of each row (the DMA lane that fills slot s fetches logical
+//    chunk s ^ f(row); a lane reading logical chunk c looks at slot c ^ f(row)):
+//      A (row pitch 2 BK = 64 or 128 bytes): f(r) = (r / rows-per-256-bytes) & (chunks - 1), so the
+//        16 rows one ds_read_b128 cycle touches land on 16 distinct 16-byte bank groups;
+//      B (row pitch 2 BN >= 128 bytes): f(k) = 4 ((k / rows-per-256-bytes) & (QB - 1)), so the 4 rows
+//        x 64 bytes of a ds_read_b64_tr_b16 cycle land on distinct bank groups.
+//    Per lane the swizzled addresses reduce to a few registers (one per 16-deep chunk for A, one per
+//    32-column tile for B) plus immediate offsets.
+//  * The MFMA B operand (A^T columns) is one ds_read_b128 per lane; the MFMA A operand (B^T rows, 8
+//    consecutive k per lane) comes from two transposing reads ds_read_b64_tr_b16 of B kept as [k][n]:
+//    in each 16-lane group, lane L addresses row k0 + (L >> 2) at columns n0 + 4 (L & 3), and result
+//    lane i then holds B[k0 + e][n0 + i] for e = 0..3. No register shuffles.
+//  * LDS fragment reads for the next 16-deep chunk are issued while the current chunk's MFMAs run
+//    (scheduling-group hints).
 //  * Workgroup ids are remapped so each XCD (own L2) walks a contiguous range of GROUP_M-grouped
 //    tiles.
 #include "fa_common.h"
@@ -26,84 +36,53 @@ namespace fa {
 typedef short g_s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) g_s16x4 g_lds_s16x4;
 
-__device__ inline u32x2 gemm_lds_read_tr16(const uint16_t* p) {
+__device__ inline u32x2 gemm_lds_read_tr16(const char* p) {
   g_s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((g_lds_s16x4*)(p));
   return __builtin_bit_cast(u32x2, r);
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmKernel {
-  static constexpr int THREADS = WM * WN * 64;
+  static constexpr int WAVES = WM * WN;
   static constexpr int TM = BM / WM / 32;  // 32-row tiles per wave along M
   static constexpr int TN = BN / WN / 32;  // 32-col tiles per wave along N
-  static constexpr int ASTR = BK + 8;      // A LDS row stride (elements): 16-byte skew
-  static constexpr int BSTR = BN + 32;     // B LDS row stride (elements): 64-byte skew
-  static constexpr int A_ELEMS = BM * ASTR;
-  static constexpr int B_ELEMS = BK * BSTR;
-  static constexpr int STAGE_ELEMS = A_ELEMS + B_ELEMS;
-  static constexpr int A_CPR = BK / 8;     // 16-byte chunks per A row
-  static constexpr int B_CPR = BN / 8;     // 16-byte chunks per B row
-  static constexpr int A_RSTEP = THREADS / A_CPR;
-  static constexpr int B_RSTEP = THREADS / B_CPR;
-  static constexpr int A_PASSES = (BM + A_RSTEP - 1) / A_RSTEP;
-  static constexpr int B_PASSES = (BK + B_RSTEP - 1) / B_RSTEP;
   static constexpr int KCH = BK / 16;      // 16-deep MFMA chunks per slab
+  static constexpr int AP = BK * 2;        // A row pitch in LDS (bytes)
+  static constexpr int BP = BN * 2;        // B row pitch in LDS (bytes)
+  static constexpr int SA = BK / 8;        // 16-byte chunks per A row
+  static constexpr int RA = 256 / AP;      // A rows per 256-byte bank line
+  static constexpr int SB = BN / 8;        // 16-byte chunks per B row
+  static constexpr int RB = BP >= 256 ? 1 : 256 / BP;  // B rows per 256-byte bank line
+  static constexpr int QB = SB / 4 < 4 ? SB / 4 : 4;   // distinct 64-byte XOR offsets for B rows
+  static constexpr int A_BYTES = BM * AP;
+  static constexpr int B_BYTES = BK * BP;
+  static constexpr int SLAB_BYTES = A_BYTES + B_BYTES;
+  // Slabs resident in LDS: as many as fit in 128 KiB, 2..4.
+  static constexpr int RING_FIT = 131072 / SLAB_BYTES;
+  static constexpr int RING = RING_FIT > 4 ? 4 : (RING_FIT < 2 ? 2 : RING_FIT);
+  static constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;  // DMA instructions per wave per slab
+  static constexpr int B_PER_WAVE = B_BYTES / 1024 / WAVES;
+  static constexpr int DMA_PER_SLAB = A_PER_WAVE + B_PER_WAVE;
   static constexpr int READS = TM + 2 * TN;  // LDS reads per chunk
-  static_assert(THREADS % A_CPR == 0 && THREADS % B_CPR == 0, "threads must cover whole rows");
   static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile shape");
+  static_assert(AP == 64 || AP == 128, "A swizzle assumes 64- or 128-byte rows");
+  static_assert(BP >= 128 && QB >= 2, "B swizzle assumes rows of at least 128 bytes");
+  static_assert(A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0, "slab must split evenly");
+  static_assert(RING * SLAB_BYTES <= 160 * 1024, "LDS");
 
-  struct Prefetch {
-    u32x4 a[A_PASSES];
-    u32x4 b[B_PASSES];
-  };
-
-  struct Ctx {
-    const uint16_t* ap;        // this thread's A chunk (row a_r0, column a_c8) of slab 0
-    const uint16_t* bp;        // this thread's B chunk (row b_r0, column b_c8) of slab 0
-    int64_t a_rstep, b_rstep;  // pointer step between passes
-    int64_t b_slab;            // pointer step between slabs for B (BK rows)
-    int a_r0, a_c8, b_r0, b_c8;
-  };
-
-  __device__ static inline void load(Prefetch& pf, const Ctx& cx, int ks) {
-    const uint16_t* a = cx.ap + ks * BK;
-    const uint16_t* b = cx.bp + ks * cx.b_slab;
-#pragma unroll
-    for (int i = 0; i < A_PASSES; ++i)
-      if (BM % A_RSTEP == 0 || cx.a_r0 + i * A_RSTEP < BM)
-        pf.a[i] = *reinterpret_cast<const u32x4*>(a + i * cx.a_rstep);
-#pragma unroll
-    for (int i = 0; i < B_PASSES; ++i)
-      if (BK % B_RSTEP == 0 || cx.b_r0 + i * B_RSTEP < BK)
-        pf.b[i] = *reinterpret_cast<const u32x4*>(b + i * cx.b_rstep);
-  }
-
-  __device__ static inline void store(const Prefetch& pf, uint16_t* as, uint16_t* bs, const Ctx& cx) {
-#pragma unroll
-    for (int i = 0; i < A_PASSES; ++i) {
-      const int row = cx.a_r0 + i * A_RSTEP;
-      if (BM % A_RSTEP == 0 || row < BM) *reinterpret_cast<u32x4*>(as + row * ASTR + cx.a_c8 * 8) = pf.a[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_PASSES; ++i) {
-      const int row = cx.b_r0 + i * B_RSTEP;
-      if (BK % B_RSTEP == 0 || row < BK) *reinterpret_cast<u32x4*>(bs + row * BSTR + cx.b_c8 * 8) = pf.b[i];
-    }
-  }
-
-  __device__ static inline void compute(floatx16 (&acc)[TN][TM], const uint16_t* as, const uint16_t* bs,
-                                        int a_off, int b_off) {
+  __device__ static inline void compute(floatx16 (&acc)[TN][TM], const char* slab, const uint32_t (&aaddr)[KCH],
+                                        const uint32_t (&baddr)[TN], int wm) {
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
       u32x4 af[TM], bf[TN];
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
-        af[tm] = *reinterpret_cast<const u32x4*>(as + a_off + tm * 32 * ASTR + c * 16);
+        af[tm] = *reinterpret_cast<const u32x4*>(slab + aaddr[c] + (wm * TM + tm) * 32 * AP);
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const uint16_t* base = bs + b_off + c * 16 * BSTR + tn * 32;
+        const char* base = slab + A_BYTES + baddr[tn] + c * 16 * BP;
         const u32x2 lo = gemm_lds_read_tr16(base);
-        const u32x2 hi = gemm_lds_read_tr16(base + 4 * BSTR);
+        const u32x2 hi = gemm_lds_read_tr16(base + 4 * BP);
         bf[tn] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
       }
 #pragma unroll
@@ -121,9 +100,10 @@ struct GemmKernel {
   }
 
   __device__ static void run(const GemmParams& p) {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE_ELEMS];
+    __shared__ __attribute__((aligned(16))) char smem[RING * SLAB_BYTES];
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, col = lane & 31, hh = lane >> 5;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hh = lane >> 5;
     const int wm = wave / WN, wn = wave % WN;
 
     const int total = p.tiles_m * p.tiles_n;
@@ -136,21 +116,63 @@ struct GemmKernel {
     const int pid_n = (pid % in_group) / gsz;
     const int m0 = pid_m * BM, n0 = pid_n * BN;
 
-    Ctx cx;
-    cx.a_r0 = tid / A_CPR;
-    cx.a_c8 = tid % A_CPR;
-    cx.b_r0 = tid / B_CPR;
-    cx.b_c8 = tid % B_CPR;
-    cx.ap = p.a + (int64_t)(m0 + cx.a_r0) * p.lda + cx.a_c8 * 8;
-    cx.bp = p.b + (int64_t)cx.b_r0 * p.ldb + n0 + cx.b_c8 * 8;
-    cx.a_rstep = (int64_t)A_RSTEP * p.lda;
-    cx.b_rstep = (int64_t)B_RSTEP * p.ldb;
-    cx.b_slab = (int64_t)BK * p.ldb;
+    // Buffer resources over this tile's A rows [m0, m0 + BM) and B columns [n0, n0 + BN), all of K
+    // (byte spans below 2^32: the host checks).
+    const u32x4 ars = make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)((int64_t)BM * p.lda * 2));
+    const u32x4 brs = make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + BN) * 2));
 
-    // Per-lane LDS fragment offsets.
-    const int a_off = ((wm * TM) * 32 + col) * ASTR + hh * 8;
-    const int g = lane & 15;
-    const int b_off = (8 * hh + (g >> 2)) * BSTR + wn * TN * 32 + 16 * ((lane >> 4) & 1) + 4 * (g & 3);
+    // DMA: the lane filling slab byte `byte` of its block fetches the logical chunk stored there.
+    uint32_t aoffs[A_PER_WAVE], boffs[B_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < A_PER_WAVE; ++j) {
+      const int byte = (wave * A_PER_WAVE + j) * 1024 + lane * 16;
+      const int r = byte / AP, s = (byte % AP) / 16;
+      const int c = s ^ ((r / RA) & (SA - 1));
+      aoffs[j] = ((uint32_t)r * (uint32_t)p.lda + c * 8) * 2u;
+    }
+#pragma unroll
+    for (int j = 0; j < B_PER_WAVE; ++j) {
+      const int byte = (wave * B_PER_WAVE + j) * 1024 + lane * 16;
+      const int k = byte / BP, s = (byte % BP) / 16;
+      const int c = s ^ (4 * ((k / RB) & (QB - 1)));
+      boffs[j] = ((uint32_t)k * (uint32_t)p.ldb + c * 8) * 2u;
+    }
+
+    // Read addresses within a slab. A: lane reads row `col` of each 32-row tile at logical chunk
+    // 2c + hh, i.e. slot (2c + hh) ^ x = (2c) ^ (hh ^ x) with x = (col / RA) & (SA - 1): the
+    // address is (col*AP + 16 (hh ^ x)) ^ 32 c; the tile's 32*AP row offset does not change x.
+    // B: lane L reads row k = 8 (L >> 5) + ((L & 15) >> 2) (+16 per chunk, +4 for the second read,
+    // neither of which changes k's swizzle term w) at logical chunk 4 jt + sb, byte 8 (L & 1) of it;
+    // slot = 4 (jt ^ w) + sb.
+    uint32_t aaddr[KCH], baddr[TN];
+    {
+      const int x = (col / RA) & (SA - 1);
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) aaddr[c] = (uint32_t)((col * AP + 16 * (hh ^ x)) ^ (32 * c));
+      const int kr = 8 * (lane >> 5) + ((lane & 15) >> 2);
+      const int sb = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      const int w = (kr / RB) & (QB - 1);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int jt = wn * TN + tn;
+        baddr[tn] = (uint32_t)(kr * BP + 64 * (jt ^ w) + 16 * sb + 8 * (lane & 1));
+      }
+    }
+
+    const uint32_t a_slab_bytes = (uint32_t)BK * 2u;                    // next K slab of A
+    const uint32_t b_slab_bytes = (uint32_t)BK * (uint32_t)p.ldb * 2u;  // next K slab of B
+    const int ksteps = p.K / BK;
+    auto issue = [&](int ks) {
+      if (ks >= ksteps) return;
+      char* slot = smem + (ks % RING) * SLAB_BYTES;
+#pragma unroll
+      for (int j = 0; j < A_PER_WAVE; ++j)
+        buffer_load16_to_lds(ars, aoffs[j] + (uint32_t)ks * a_slab_bytes, slot + (wave * A_PER_WAVE + j) * 1024);
+#pragma unroll
+      for (int j = 0; j < B_PER_WAVE; ++j)
+        buffer_load16_to_lds(brs, boffs[j] + (uint32_t)ks * b_slab_bytes,
+                             slot + A_BYTES + (wave * B_PER_WAVE + j) * 1024);
+    };
 
     floatx16 acc[TN][TM];
 #pragma unroll
@@ -160,21 +182,18 @@ struct GemmKernel {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[tn][tm][r] = 0.f;
 
-    Prefetch pf;
-    load(pf, cx, 0);
-    store(pf, smem, smem + A_ELEMS, cx);
-    __syncthreads();
+#pragma unroll
+    for (int s = 0; s + 1 < RING; ++s) issue(s);
+    wait_vm_lds_barrier<0>();
 
-    const int ksteps = p.K / BK;
     for (int ks = 0; ks < ksteps; ++ks) {
-      const uint16_t* as = smem + (ks & 1) * STAGE_ELEMS;
-      if (ks + 1 < ksteps) load(pf, cx, ks + 1);
-      compute(acc, as, as + A_ELEMS, a_off, b_off);
-      if (ks + 1 < ksteps) {
-        uint16_t* an = smem + ((ks + 1) & 1) * STAGE_ELEMS;
-        store(pf, an, an + A_ELEMS, cx);
-      }
-      __syncthreads();
+      issue(ks + RING - 1);  // into the slot slab ks-1 left (read in step ks-1)
+      compute(acc, smem + (ks % RING) * SLAB_BYTES, aaddr, baddr, wm);
+      // Step ks+1 reads slab ks+1; the RING-2 newer slabs may stay in flight.
+      if (RING > 2 && ks + RING - 1 < ksteps)
+        wait_vm_lds_barrier<(RING > 2 ? (RING - 2) * DMA_PER_SLAB : 0)>();
+      else
+        wait_vm_lds_barrier<0>();
     }
 
     // C^T tile: lane holds row m = ...+col, columns n = 8*gq + 4*hh + 0..3 of each 32-col tile.
