@@ -748,12 +748,20 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 1)
 
+// D = 256, pipelined with 32-key tiles: Q (64 registers) and O (128) leave room for two 32-key
+// score tiles; a step then has the MFMA count and LDS bytes of a 64-key D = 128 step with half
+// its softmax work per MFMA.
+#define FA_ENTRIES_D256_PIPE(TAG, DTYPE)                    \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 0),                \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 1)
+
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 256),   FA_ENTRIES_D(bf16_t, FA_DTYPE_BF16, 64),
     FA_ENTRIES_D(bf16_t, FA_DTYPE_BF16, 128), FA_ENTRIES_D(bf16_t, FA_DTYPE_BF16, 256),
     FA_ENTRIES_D_WIDE(f16_t, FA_DTYPE_F16, 64), FA_ENTRIES_D_WIDE(f16_t, FA_DTYPE_F16, 128),
     FA_ENTRIES_D_WIDE(bf16_t, FA_DTYPE_BF16, 64), FA_ENTRIES_D_WIDE(bf16_t, FA_DTYPE_BF16, 128),
+    FA_ENTRIES_D256_PIPE(f16_t, FA_DTYPE_F16), FA_ENTRIES_D256_PIPE(bf16_t, FA_DTYPE_BF16),
 };
 
 static const FaMergeEntry kMergeEntries[] = {

@@ -40,6 +40,7 @@ VARIANT_BY_KERNEL = {
 FA_TILE_SPACE = [
     (128, 64, 4, 3),
     (256, 64, 8, 3),
+    (128, 32, 4, 3),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),

@@ -28,6 +28,7 @@ TILES = {
     # software-pipelined kernel (stages=3): LDS-DMA ring of 2 tiles (4 waves) or 3 tiles (8 waves)
     "pipe128": (OPT, 128, 64, 4, 3),
     "pipe256": (OPT, 256, 64, 8, 3),
+    "pipe128n32": (OPT, 128, 32, 4, 3),  # D = 256 pipelined (32-key tiles)
 }
 
 
@@ -74,6 +75,9 @@ CASES = [
     ("pipe_ragged", 2, 3, 3, 200, 333, 128, F16, False, "pipe128"),
     ("pipe_w8_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "pipe256"),
     ("pipe_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pipe256"),
+    ("pipe_d256_bf16", 1, 2, 2, 256, 300, 256, BF16, False, "pipe128n32"),
+    ("pipe_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "pipe128n32"),
+    ("pipe_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "pipe128n32"),
 ]
 
 

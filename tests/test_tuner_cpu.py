@@ -11,6 +11,7 @@ import torch
 import exceptions
 import flash_atten
 import gfx950_configs as cfgs
+import hip_lib
 import mma
 import tuner
 from tuner import (
@@ -320,5 +321,8 @@ def test_every_candidate_has_compiled_resources():
                 for c in cands:
                     res = cfgs.fa_resources(variant, dtype, D, c)
                     assert res is not None and res["lds_bytes"] <= 160 * 1024
+                    # the resources are those of the candidate's own pipeline
+                    sym = hip_lib.fwd_kernel_symbol(variant, dtype, D, c.to_c())
+                    assert f"ELi{c.block_n}ELi{c.stages}ELb" in sym, (sym, c)
     for t in cfgs.gemm_candidates():
         assert cfgs.gemm_resources(t) is not None
