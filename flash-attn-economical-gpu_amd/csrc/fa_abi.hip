@@ -263,9 +263,10 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   if (M < 0 || N < 0 || K < 0) return fail(FA_EINVAL, "negative GEMM size");
   if (M == 0 || N == 0) return ok();
   if (K == 0) return fail(FA_EINVAL, "K=0 is not supported (the reference requires K %% 32 == 0, K > 0)");
-  if (M % e->block_m || N % e->block_n || K % e->block_k)
-    return fail(FA_EINVAL, "M=%d N=%d K=%d must be multiples of the %dx%dx%d tile", M, N, K, e->block_m,
-                e->block_n, e->block_k);
+  // Any M; N and K need only whole 8-byte output groups and 16-byte K chunks (the reference's
+  // divisibility rule, mma.py:76-81, is kept by the drop-in selector, not here).
+  if (K % 8 || N % 4)
+    return fail(FA_EINVAL, "K=%d must be a multiple of 8 and N=%d a multiple of 4", K, N);
   if (!a || !b || !c) return fail(FA_EINVAL, "null GEMM pointer");
   if (!aligned16(a) || !aligned16(b) || (reinterpret_cast<uintptr_t>(c) & 7u))
     return fail(FA_EINVAL, "A and B must be 16-byte aligned, C 8-byte aligned");
@@ -274,9 +275,9 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
                 (long long)ldb, (long long)ldc);
   if (tile->group_m < 1) return fail(FA_EINVAL, "group_m must be >= 1");
   // The kernel addresses a tile's A rows and B columns (all of K) as raw buffers with 32-bit byte
-  // offsets.
-  if ((int64_t)e->block_m * lda * 2 > 0xffffffffLL || ((int64_t)(K - 1) * ldb + e->block_n) * 2 > 0xffffffffLL)
-    return fail(FA_ENOTSUP, "GEMM operand spans beyond 4 GiB per tile (lda=%lld ldb=%lld K=%d)", (long long)lda,
+  // offsets, and uses 2^31 as its out-of-range offset.
+  if ((int64_t)e->block_m * lda * 2 > 0x7fffffffLL || ((int64_t)(K - 1) * ldb + N) * 2 > 0x7fffffffLL)
+    return fail(FA_ENOTSUP, "GEMM operand spans beyond 2 GiB per tile (lda=%lld ldb=%lld K=%d)", (long long)lda,
                 (long long)ldb, K);
   fa::GemmParams p;
   p.a = static_cast<const uint16_t*>(a);
@@ -285,8 +286,8 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   p.M = M; p.N = N; p.K = K;
   p.lda = lda; p.ldb = ldb; p.ldc = ldc;
   p.group_m = tile->group_m;
-  p.tiles_m = M / e->block_m;
-  p.tiles_n = N / e->block_n;
+  p.tiles_m = (M + e->block_m - 1) / e->block_m;
+  p.tiles_n = (N + e->block_n - 1) / e->block_n;
   const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
   if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large");
   void* kargs[] = {&p};

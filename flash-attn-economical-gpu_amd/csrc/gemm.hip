@@ -116,19 +116,24 @@ struct GemmKernel {
     const int pid_n = (pid % in_group) / gsz;
     const int m0 = pid_m * BM, n0 = pid_n * BN;
 
-    // Buffer resources over this tile's A rows [m0, m0 + BM) and B columns [n0, n0 + BN), all of K
-    // (byte spans below 2^32: the host checks).
-    const u32x4 ars = make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)((int64_t)BM * p.lda * 2));
-    const u32x4 brs = make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + BN) * 2));
+    // Buffer resources over this tile's A rows [m0, min(m0 + BM, M)) and B columns [n0, n0 + BN)
+    // of rows [0, K) (byte spans below 2^31: the host checks). Loads past the ranges return zeros:
+    // rows of A past M and rows of B past K need no branch. Columns of B past N read neighbouring
+    // data of the same rows (finite) and only reach output columns that are not stored.
+    const int m_rows = min(BM, p.M - m0);
+    const u32x4 ars = make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)((int64_t)m_rows * p.lda * 2));
+    const u32x4 brs = make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + (p.N - n0)) * 2));
 
     // DMA: the lane filling slab byte `byte` of its block fetches the logical chunk stored there.
     uint32_t aoffs[A_PER_WAVE], boffs[B_PER_WAVE];
+    int ak0[A_PER_WAVE];  // first k of the A chunk this lane moves (within a slab)
 #pragma unroll
     for (int j = 0; j < A_PER_WAVE; ++j) {
       const int byte = (wave * A_PER_WAVE + j) * 1024 + lane * 16;
       const int r = byte / AP, s = (byte % AP) / 16;
       const int c = s ^ ((r / RA) & (SA - 1));
       aoffs[j] = ((uint32_t)r * (uint32_t)p.lda + c * 8) * 2u;
+      ak0[j] = c * 8;
     }
 #pragma unroll
     for (int j = 0; j < B_PER_WAVE; ++j) {
@@ -161,13 +166,20 @@ struct GemmKernel {
 
     const uint32_t a_slab_bytes = (uint32_t)BK * 2u;                    // next K slab of A
     const uint32_t b_slab_bytes = (uint32_t)BK * (uint32_t)p.ldb * 2u;  // next K slab of B
-    const int ksteps = p.K / BK;
+    const int ksteps = (p.K + BK - 1) / BK;
+    const bool k_ragged = (p.K % BK) != 0;  // last slab runs past K: A chunks there read zeros
     auto issue = [&](int ks) {
       if (ks >= ksteps) return;
       char* slot = smem + (ks % RING) * SLAB_BYTES;
+      const bool tail = k_ragged && ks == ksteps - 1;
 #pragma unroll
-      for (int j = 0; j < A_PER_WAVE; ++j)
-        buffer_load16_to_lds(ars, aoffs[j] + (uint32_t)ks * a_slab_bytes, slot + (wave * A_PER_WAVE + j) * 1024);
+      for (int j = 0; j < A_PER_WAVE; ++j) {
+        // past-K chunks of the ragged slab get an offset beyond the range (zeros): A's rows may hold
+        // anything there, and 0 * NaN would reach valid outputs. 2^31 is past every range (the host
+        // keeps spans below 2 GiB) and far from 32-bit wrap-around.
+        const uint32_t off = (tail && ks * BK + ak0[j] >= p.K) ? 0x80000000u : aoffs[j] + (uint32_t)ks * a_slab_bytes;
+        buffer_load16_to_lds(ars, off, slot + (wave * A_PER_WAVE + j) * 1024);
+      }
 #pragma unroll
       for (int j = 0; j < B_PER_WAVE; ++j)
         buffer_load16_to_lds(brs, boffs[j] + (uint32_t)ks * b_slab_bytes,
@@ -196,16 +208,19 @@ struct GemmKernel {
         wait_vm_lds_barrier<0>();
     }
 
-    // C^T tile: lane holds row m = ...+col, columns n = 8*gq + 4*hh + 0..3 of each 32-col tile.
+    // C^T tile: lane holds row m = ...+col, columns n = 8*gq + 4*hh + 0..3 of each 32-col tile
+    // (N % 4 == 0, so each 4-column group is wholly inside or outside the matrix).
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
       const int m = m0 + (wm * TM + tm) * 32 + col;
+      if (m >= p.M) continue;
       uint16_t* crow = p.c + (int64_t)m * p.ldc + n0;
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const int n = (wn * TN + tn) * 32 + 8 * gq + 4 * hh;
+          if (n0 + n >= p.N) continue;
           u32x2 val = {DT<f16_t>::pack2(acc[tn][tm][4 * gq], acc[tn][tm][4 * gq + 1]),
                        DT<f16_t>::pack2(acc[tn][tm][4 * gq + 2], acc[tn][tm][4 * gq + 3])};
           *reinterpret_cast<u32x2*>(crow + n) = val;

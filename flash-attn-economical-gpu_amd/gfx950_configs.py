@@ -263,6 +263,28 @@ def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None =
     return (*t, _gemm_group_m(M, N, K, t))
 
 
+def choose_gemm_tile_any(M: int, N: int, K: int) -> tuple[int, int, int, int, int]:
+    """(block_m, block_n, block_k, waves, group_m) for any shape the kernel accepts (K % 8 == 0,
+    N % 4 == 0; partial tiles in M, N and K are masked in the kernel): the divisible choice when
+    there is one, else the tuned tile of the shape's bucket, else the first built tile no larger
+    than the problem (rounded up to 64)."""
+    if K % 8 != 0 or N % 4 != 0:
+        raise ValueError(f"gfx950 GEMM needs K % 8 == 0 and N % 4 == 0 (got M={M} N={N} K={K})")
+    try:
+        return choose_gemm_tile(M, N, K)
+    except ValueError:
+        pass
+    cands = gemm_candidates()
+    entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
+    if entry is not None:
+        for t in cands:
+            if list(t) == list(entry["tile"]):
+                return (*t, int(entry.get("group_m", GEMM_DEFAULT_GROUP_M)))
+    fit = [t for t in cands if t[0] <= -(-M // 64) * 64 and t[1] <= -(-N // 64) * 64]
+    t = (fit or [min(cands, key=lambda t: t[0] * t[1])])[0]
+    return (*t, GEMM_DEFAULT_GROUP_M)
+
+
 def _gemm_group_m(M: int, N: int, K: int, tile) -> int:
     entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
     if entry is not None and list(entry["tile"]) == list(tile):

@@ -30,7 +30,11 @@ logger = logging.getLogger(__name__)
 
 @functools.lru_cache(maxsize=1024)
 def _gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None, group_m: int | None):
-    bm, bn, bk, waves, gm = cfgs.choose_gemm_tile(M, N, K, hint)
+    try:
+        bm, bn, bk, waves, gm = cfgs.choose_gemm_tile(M, N, K, hint)
+    except ValueError:
+        # no built tile divides the shape: the kernel masks partial tiles (K % 8, N % 4 suffice)
+        bm, bn, bk, waves, gm = cfgs.choose_gemm_tile_any(M, N, K)
     return hip_lib.GemmTile(bm, bn, bk, waves, int(group_m) if group_m else gm)
 
 
@@ -93,17 +97,18 @@ def _select_2d_contiguous_config(m: int, n: int, k: int) -> tuple[int, int, int,
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """C = A @ B through the gfx950 kernel (convenience entry)."""
+    """C = A @ B through the gfx950 kernel (convenience entry). Unlike the reference selector it
+    accepts shapes no tile divides (K % 8 == 0 and N % 4 == 0; partial tiles are masked)."""
     a = a.contiguous()
     b = b.contiguous()
     M, K = a.shape
     _, N = b.shape
     c = torch.empty((M, N), device=a.device, dtype=torch.float16) if out is None else out
-    bm, bn, bk, group_m, waves, stages = _select_2d_contiguous_config(M, N, K)
-    _matmul_contiguous_kernel[(M // bm * (N // bn),)](
+    bm, bn, bk, waves, group_m = cfgs.choose_gemm_tile_any(M, N, K)
+    _matmul_contiguous_kernel[(-(-M // bm) * -(-N // bn),)](
         a, b, c, M, N, K, BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=group_m,
         USE_CACHE_EVICTION_HINTS=_supports_contiguous_cache_eviction_hints(a.device),
-        num_warps=waves, num_stages=stages,
+        num_warps=waves, num_stages=2,
     )
     return c
 

@@ -117,7 +117,7 @@ def test_fa_fwd_empty_problem_is_a_no_op():
 
 @pytest.mark.parametrize(
     "dims,code",
-    [((256, 256, 100), hip_lib.FA_EINVAL), ((200, 256, 256), hip_lib.FA_EINVAL), ((256, 256, 0), hip_lib.FA_EINVAL),
+    [((256, 256, 100), hip_lib.FA_EINVAL), ((256, 254, 256), hip_lib.FA_EINVAL), ((256, 256, 0), hip_lib.FA_EINVAL),
      ((0, 256, 256), hip_lib.FA_OK)],
 )
 def test_gemm_rejects_before_launch(dims, code):
