@@ -115,3 +115,28 @@ def test_live_sweep_writes_selectable_entries(gpu, tmp_path, monkeypatch, fresh_
         got = cfgs.choose_fa_tile(variant, dtype, D, causal, 1, bh, m, n, cfgs.fa_candidates(variant, dtype, D))
         assert [got.block_m, got.block_n, got.waves, got.stages] == entry["tile"]
     assert list(cfgs.choose_gemm_tile(256, 256, 256)[:4]) == table["gemm"][cfgs.gemm_table_key(256, 256, 256)]["tile"]
+
+
+def test_case_log_lines_parse_like_the_reference_log():
+    """case_log.py writes the `[case]` layout the reference's pipeline-log parser reads
+    (test_flash_atten.py:270-305): shape fields, then `<series> ... mean=<ms>ms` per series, n/a for
+    series that did not run. The two patterns below are that parser's, applied to our line."""
+    import re
+
+    import case_log
+
+    stats = {"triton_flash_basic": {"mean_ms": 1.5, "p50_ms": 1.4},
+             "triton_flash_opt_shared_mem": {"mean_ms": 1.25, "p50_ms": 1.2},
+             "triton_flash_block_d_nomask": {"mean_ms": 1.0, "p50_ms": 0.9},
+             "gpu_flash_sdpa": {"mean_ms": 2.5, "p50_ms": 2.4}}
+    line = case_log.format_case_line((1, 28, 128, 8192, False), stats,
+                                     {"gpu_math_sdpa": "skipped(size)", "triton_flash_basic": "max_abs_diff=1.00e-03"})
+    assert line.startswith("[case]")
+    shape = re.search(r"\bB=(\d+)\s+H=(\d+)\s+S=(\d+)\s+D=(\d+)\s+causal=(True|False)\b", line)
+    assert shape.groups() == ("1", "28", "8192", "128", "False")
+    got = {}
+    for name in case_log.SERIES:
+        m = re.search(rf"(?:^|\|\s*){re.escape(name)}(?:\s+[^|]*?)?\s+mean=(n/a|[0-9.]+)ms\b", line)
+        got[name] = None if m is None or m.group(1) == "n/a" else float(m.group(1))
+    assert got == {"cpu_sdpa": None, "gpu_math_sdpa": None, "gpu_efficient_sdpa": None, "gpu_flash_sdpa": 2.5,
+                   "triton_flash_basic": 1.5, "triton_flash_opt_shared_mem": 1.25, "triton_flash_block_d_nomask": 1.0}
