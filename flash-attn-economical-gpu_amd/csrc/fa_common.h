@@ -116,13 +116,20 @@ __device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
 // LDS-DMA in flight before each LDS read; the kernel waits explicitly (wait_vm_lds_barrier).
 // vmcnt retires in order, so the compiler's own vmcnt waits stay correct (they can only wait
 // longer when these loads are outstanding).
-__device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, const void* lds_block) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_block);
+// `lds_block` is the block's LDS byte address (lds_address of the __shared__ array plus a
+// wave-uniform offset), so M0 is computed with scalar instructions.
+__device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_block);
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
                :
                : "v"(byte_off), "s"(lds), "s"(rsrc)
                : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ array (the generic -> LDS cast of the array itself folds to a
+// constant; casting a computed generic pointer would add a null check).
+__device__ inline uint32_t lds_address(const void* shared_array) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)shared_array;
 }
 
 // Wait until at most N vector-memory operations of this wave are outstanding and all its LDS

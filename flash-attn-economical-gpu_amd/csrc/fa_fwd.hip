@@ -500,19 +500,23 @@ struct FwdKernel {
         const uint32_t c0 = dt * 32 + 16 * ((m >> 3) & 1) + 8 * (m & 1);
         voffs[j] = (row * (uint32_t)p.sv2 + c0) * 2u;
       }
+      // DMA destinations as LDS byte addresses from the wave index in a scalar register: M0 is
+      // then computed with scalar instructions only.
+      const uint32_t kring_lds = lds_address(smem), vring_lds = kring_lds + RING * KT_ELEMS * 2;
+      const int wave_u = __builtin_amdgcn_readfirstlane(wave);
       auto issue_k = [&](int u) {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
-        uint16_t* slot = kring + (u % RING) * KT_ELEMS;
+        const uint32_t slot = kring_lds + (uint32_t)(u % RING) * (KT_ELEMS * 2);
 #pragma unroll
-        for (int j = 0; j < NKW; ++j) buffer_load16_to_lds(krs, koffs[j] + toff, slot + (wave * NKW + j) * 512);
+        for (int j = 0; j < NKW; ++j) buffer_load16_to_lds(krs, koffs[j] + toff, slot + (wave_u * NKW + j) * 1024);
       };
       auto issue_v = [&](int u) {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
-        uint16_t* slot = vring + (u % RING) * VT_ELEMS;
+        const uint32_t slot = vring_lds + (uint32_t)(u % RING) * (VT_ELEMS * 2);
 #pragma unroll
-        for (int j = 0; j < NVW; ++j) buffer_load16_to_lds(vrs, voffs[j] + toff, slot + (wave * NVW + j) * 512);
+        for (int j = 0; j < NVW; ++j) buffer_load16_to_lds(vrs, voffs[j] + toff, slot + (wave_u * NVW + j) * 1024);
       };
       const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
       const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block

@@ -168,9 +168,11 @@ struct GemmKernel {
     const uint32_t b_slab_bytes = (uint32_t)BK * (uint32_t)p.ldb * 2u;  // next K slab of B
     const int ksteps = (p.K + BK - 1) / BK;
     const bool k_ragged = (p.K % BK) != 0;  // last slab runs past K: A chunks there read zeros
+    const uint32_t smem_lds = lds_address(smem);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // scalar DMA destinations
     auto issue = [&](int ks) {
       if (ks >= ksteps) return;
-      char* slot = smem + (ks % RING) * SLAB_BYTES;
+      const uint32_t slot = smem_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
       const bool tail = k_ragged && ks == ksteps - 1;
 #pragma unroll
       for (int j = 0; j < A_PER_WAVE; ++j) {
@@ -178,12 +180,12 @@ struct GemmKernel {
         // anything there, and 0 * NaN would reach valid outputs. 2^31 is past every range (the host
         // keeps spans below 2 GiB) and far from 32-bit wrap-around.
         const uint32_t off = (tail && ks * BK + ak0[j] >= p.K) ? 0x80000000u : aoffs[j] + (uint32_t)ks * a_slab_bytes;
-        buffer_load16_to_lds(ars, off, slot + (wave * A_PER_WAVE + j) * 1024);
+        buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
       }
 #pragma unroll
       for (int j = 0; j < B_PER_WAVE; ++j)
         buffer_load16_to_lds(brs, boffs[j] + (uint32_t)ks * b_slab_bytes,
-                             slot + A_BYTES + (wave * B_PER_WAVE + j) * 1024);
+                             slot + A_BYTES + (wave_u * B_PER_WAVE + j) * 1024);
     };
 
     floatx16 acc[TN][TM];
