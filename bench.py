@@ -288,7 +288,7 @@ def main() -> int:
     gemm_tflops = gemm_flops / (g_total / args.steps * 1e-3) / 1e12
     ref = a.float() @ b.float()
     gemm_rel = ((c.float() - ref).norm() / ref.norm()).item()
-    _log(f"gemm {bm}x{bn}x{bk}: {g_total / args.steps:.3f} ms, {gemm_tflops:.1f} TFLOP/s, rel_fro={gemm_rel:.2e}")
+    _log(f"gemm {bm}x{bn}x{bk} waves={warps} group_m={group_m}: {g_total / args.steps:.3f} ms, {gemm_tflops:.1f} TFLOP/s, rel_fro={gemm_rel:.2e}")
     del a, b, c, ref
     torch.cuda.empty_cache()
 
@@ -341,7 +341,7 @@ def main() -> int:
             "metric": "GEMM fp16 TFLOP/s at 8192^3",
             "value": round(gemm_tflops, 2),
             "ms_per_step": round(g_total / args.steps, 4),
-            "tile": [bm, bn, bk, group_m],
+            "tile": {"block_m": bm, "block_n": bn, "block_k": bk, "waves": warps, "group_m": group_m},
             "roofline": {
                 "bound": "mfma",
                 "achieved": round(gemm_flops / (gemm_launch_ms * 1e-3) / 1e12, 2),

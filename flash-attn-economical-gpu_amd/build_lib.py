@@ -5,7 +5,8 @@ Usage: python build_lib.py [--jobs N]
 Each csrc/*.hip file is compiled to an object in _build/ (in parallel), then linked into
 libfa_gfx950.so next to this file. The compiler's kernel-resource-usage remarks are parsed into
 kernel_resources.json (VGPR/AGPR/SGPR counts, LDS bytes, scratch, occupancy per kernel symbol), which
-the tuner's resource filter and the resource report read on hosts without a GPU.
+the tuner's resource filter and the resource report read on hosts without a GPU. Measurement
+programs under probes/ (not part of the library) are built into executables next to their sources.
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
+PROBES = HERE / "probes"
 LIB = HERE / "libfa_gfx950.so"
 RESOURCES = HERE / "kernel_resources.json"
 ARCH = "gfx950"
@@ -115,7 +117,25 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     RESOURCES.write_text(json.dumps(resources, indent=1, sort_keys=True) + "\n")
     if verbose:
         print(f"[build] linked {LIB} ({len(resources)} kernels with resource data)", flush=True)
+    for exe in build_probes():
+        if verbose:
+            print(f"[build] probe {exe}", flush=True)
     return LIB
+
+
+def build_probes() -> list[Path]:
+    """Standalone measurement programs (probes/*.hip -> probes/<name>); not part of the library."""
+    built = []
+    for src in sorted(PROBES.glob("*.hip")):
+        exe = PROBES / src.stem
+        cmd = [_hipcc(), *(f for f in HIPCC_FLAGS if not f.startswith("-Rpass") and f != "-fPIC"), "-o", str(exe),
+               str(src)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            sys.stderr.write(proc.stderr)
+            raise RuntimeError(f"hipcc failed for probe {src.name} (exit {proc.returncode})")
+        built.append(exe)
+    return built
 
 
 if __name__ == "__main__":
