@@ -173,6 +173,18 @@ struct FwdKernel {
     }
   }
 
+  // Kernels with one wave per SIMD keep O in AGPRs (the MFMAs accumulate there directly). The rare
+  // rescale needs O in VGPRs; pinning O to AGPRs on both sides of it keeps the AGPR <-> VGPR copies
+  // inside the rescale branch. Without the pins the compiler hoisted them to the loop header, where
+  // 144 v_accvgpr_read ran on every step of the D = 256 kernel (~15% of its time).
+  static constexpr bool kAccInAgpr = RT > 1 || D > 128;  // more than 256 registers per lane
+  __device__ static inline void pin_acc_agpr(floatx16 (&acc)[DTL][RT], int rt) {
+    if constexpr (kAccInAgpr) {
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) asm volatile("" : "+a"(acc[dt][rt]));
+    }
+  }
+
   // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some row of the
   // wave sees a max more than THRESH (log2 units) above it.
   __device__ static inline void rescale(const float (&mx)[RT], floatx16 (&acc)[DTL][RT], float (&m_use)[RT],
@@ -185,10 +197,12 @@ struct FwdKernel {
         const float alpha = (m_use[rt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[rt] - m_new) * c);
         m_use[rt] = m_new;
         l_i[rt] *= alpha;
+        pin_acc_agpr(acc, rt);
 #pragma unroll
         for (int dt = 0; dt < DTL; ++dt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[dt][rt][r] *= alpha;
+        pin_acc_agpr(acc, rt);
       }
     }
   }
