@@ -106,6 +106,25 @@ const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_til
   return e;
 }
 
+// GEMM tile regions per XCD: the split of the tile grid into region_m x (8 / region_m) equal
+// rectangles whose A + B panel footprint (rows * block_m + columns * block_n) is smallest, or 0
+// (flat grouped order) when no split divides the grid.
+int gemm_region_rows(int tiles_m, int tiles_n, int block_m, int block_n) {
+  constexpr int kXcds = 8;
+  int best = 0;
+  int64_t best_cost = 0;
+  for (int rm = 1; rm <= kXcds; rm *= 2) {
+    const int rn = kXcds / rm;
+    if (tiles_m % rm != 0 || tiles_n % rn != 0) continue;
+    const int64_t cost = (int64_t)(tiles_m / rm) * block_m + (int64_t)(tiles_n / rn) * block_n;
+    if (best == 0 || cost < best_cost) {
+      best = rm;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 extern "C" {
@@ -290,6 +309,7 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   p.tiles_n = (N + e->block_n - 1) / e->block_n;
   const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
   if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large");
+  p.region_m = gemm_region_rows(p.tiles_m, p.tiles_n, e->block_m, e->block_n);
   void* kargs[] = {&p};
   hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0,
                                    static_cast<hipStream_t>(stream));

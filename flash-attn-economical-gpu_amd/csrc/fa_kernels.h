@@ -74,6 +74,7 @@ struct GemmParams {
   int64_t lda, ldb, ldc;
   int32_t group_m;
   int32_t tiles_m, tiles_n;
+  int32_t region_m;  // 0: flat grouped order; else XCD regions in region_m rows x (8 / region_m) columns
 };
 
 struct GemmKernelEntry {

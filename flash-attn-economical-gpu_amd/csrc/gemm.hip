@@ -2,7 +2,9 @@
 //
 // Replaces the reference's Triton `_matmul_contiguous_kernel` (mma.py:8-52): grouped tile order
 // with GROUP_M rows of tiles per group (mma.py:22-30), fp32 accumulate over K (mma.py:39-49),
-// fp16 store (mma.py:51-52), no masks (M, N, K multiples of the tile).
+// fp16 store (mma.py:51-52). The reference needs M, N, K to be multiples of the tile; here partial
+// tiles are masked (loads past M, N or K read zeros, stores outside [M, N) are skipped), so any M
+// with K % 8 == 0 and N % 4 == 0 runs.
 //
 // gfx950 design:
 //  * v_mfma_f32_32x32x16_f16 computes C^T = B^T A^T per 32x32 tile, so the accumulator gives each
@@ -26,8 +28,9 @@
 //    lane i then holds B[k0 + e][n0 + i] for e = 0..3. No register shuffles.
 //  * LDS fragment reads for the next 16-deep chunk are issued while the current chunk's MFMAs run
 //    (scheduling-group hints).
-//  * Workgroup ids are remapped so each XCD (own L2) walks a contiguous range of GROUP_M-grouped
-//    tiles.
+//  * Each XCD (own L2) walks one rectangle of the tile grid in GROUP_M-grouped order (the split with
+//    the smallest A + B panel footprint, chosen by the host), or, when the grid does not split into
+//    8 equal rectangles, a contiguous range of the flat grouped order.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -106,14 +109,30 @@ struct GemmKernel {
     const int col = lane & 31, hh = lane >> 5;
     const int wm = wave / WN, wn = wave % WN;
 
-    const int total = p.tiles_m * p.tiles_n;
-    const int pid = xcd_remap(blockIdx.x, total);
-    const int in_group = p.group_m * p.tiles_n;
-    const int group_id = pid / in_group;
-    const int first_m = group_id * p.group_m;
-    const int gsz = min(p.tiles_m - first_m, p.group_m);
-    const int pid_m = first_m + (pid % in_group) % gsz;
-    const int pid_n = (pid % in_group) / gsz;
+    int pid_m, pid_n;
+    if (p.region_m > 0) {
+      // XCD x (workgroups are dispatched round-robin: blockIdx % 8) owns one rectangle of tiles,
+      // region (x / rn, x % rn) of a region_m x rn split, and walks it in GROUP_M-grouped order:
+      // each XCD's L2 then sees tiles_m / region_m A panels and tiles_n / rn B panels instead of
+      // every B panel.
+      constexpr int kXcds = 8;
+      const int rn = kXcds / p.region_m;
+      const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+      const int rt_m = p.tiles_m / p.region_m, rt_n = p.tiles_n / rn;
+      const int in_group = p.group_m * rt_n;
+      const int first_m = (slot / in_group) * p.group_m;
+      const int gsz = min(rt_m - first_m, p.group_m);
+      pid_m = (xcd / rn) * rt_m + first_m + (slot % in_group) % gsz;
+      pid_n = (xcd % rn) * rt_n + (slot % in_group) / gsz;
+    } else {
+      const int total = p.tiles_m * p.tiles_n;
+      const int pid = xcd_remap(blockIdx.x, total);
+      const int in_group = p.group_m * p.tiles_n;
+      const int first_m = (pid / in_group) * p.group_m;
+      const int gsz = min(p.tiles_m - first_m, p.group_m);
+      pid_m = first_m + (pid % in_group) % gsz;
+      pid_n = (pid % in_group) / gsz;
+    }
     const int m0 = pid_m * BM, n0 = pid_n * BN;
 
     // Buffer resources over this tile's A rows [m0, min(m0 + BM, M)) and B columns [n0, n0 + BN)
