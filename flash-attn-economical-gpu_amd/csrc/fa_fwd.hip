@@ -254,7 +254,9 @@ struct FwdKernel {
   // Scheduling hints (apply to the basic block they are emitted in): issue the LDS fragment reads
   // a few MFMAs ahead of their use instead of waiting on each read right before its MFMA.
   static constexpr int kReadAheadK = 4;  // K fragments (one ds_read_b128 each)
-  static constexpr int kReadAheadV = 2;  // V fragments (two ds_read_b64_tr_b16 each)
+  // V fragments (two ds_read_b64_tr_b16 each); one wave per SIMD (D = 256) has no second wave to
+  // hide LDS latency and, with Q and O in AGPRs, the VGPRs to read further ahead
+  static constexpr int kReadAheadV = kAccInAgpr ? 4 : 2;
   __device__ static inline void qk_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x100, kReadAheadK, 0);  // DS read
 #pragma unroll
@@ -422,6 +424,14 @@ struct FwdKernel {
         if (row < rows) val = *reinterpret_cast<const u32x4*>(qrow + cc * 16 + hh * 8);
         qf[rt][cc] = val;
       }
+    }
+    if constexpr (kAccInAgpr) {
+      // Q is only ever an MFMA operand, which may sit in AGPRs: this leaves VGPRs for fragment
+      // read-ahead in the one-wave-per-SIMD kernels.
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int cc = 0; cc < DC; ++cc) asm volatile("" : "+a"(qf[rt][cc]));
     }
 
     // KV tiles of this split, clipped by the causal diagonal.
