@@ -117,13 +117,26 @@ __device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
 // vmcnt retires in order, so the compiler's own vmcnt waits stay correct (they can only wait
 // longer when these loads are outstanding).
 // `lds_block` is the block's LDS byte address (lds_address of the __shared__ array plus a
-// wave-uniform offset), so M0 is computed with scalar instructions.
+// wave-uniform offset), so M0 is computed with scalar instructions. IMM is added to byte_off by the
+// instruction's 12-bit offset field (the range check applies to the sum).
+template <int IMM = 0>
 __device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
+  static_assert(IMM >= 0 && IMM < 4096, "12-bit immediate offset");
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_block);
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen offset:%3 lds"
                :
-               : "v"(byte_off), "s"(lds), "s"(rsrc)
+               : "v"(byte_off), "s"(lds), "s"(rsrc), "n"(IMM)
                : "memory", "m0");
+}
+
+// N consecutive 1 KiB blocks whose per-lane sources are STEP bytes apart: one offset register, the
+// steps in the immediate field.
+template <int N, int STEP, int J = 0>
+__device__ inline void buffer_load16_to_lds_blocks(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
+  if constexpr (J < N) {
+    buffer_load16_to_lds<J * STEP>(rsrc, byte_off, lds_block + J * 1024u);
+    buffer_load16_to_lds_blocks<N, STEP, J + 1>(rsrc, byte_off, lds_block);
+  }
 }
 
 // LDS byte address of a __shared__ array (the generic -> LDS cast of the array itself folds to a

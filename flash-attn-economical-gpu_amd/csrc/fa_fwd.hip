@@ -9,7 +9,8 @@
 //    v_mfma_f32_32x32x16: the accumulator then gives every lane ONE query row (lane & 31) and 16
 //    keys per 32x32 tile, so the row max / sum / rescale factor are per-lane scalars and the only
 //    cross-lane step is one exchange between the two half-waves.
-//  * Q^T is the B operand and stays in VGPRs for the whole kernel (loaded once).
+//  * Q^T is the B operand and stays in registers for the whole kernel (loaded once; AGPRs in the
+//    kernels with one wave per SIMD).
 //  * P^T is fed to O^T = V^T P^T directly from the S^T accumulator registers (the B-operand k-slots
 //    of a 16-key chunk are exactly 8 accumulator rows the lane already holds), so P never goes
 //    through LDS. V^T is the A operand, read from V stored naturally ([key][d]) in LDS with the
@@ -374,7 +375,8 @@ struct FwdKernel {
     __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, col = lane & 31, hh = lane >> 5;
+    // wave index in a scalar register: wave-uniform row bounds and mask tests stay scalar
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), col = lane & 31, hh = lane >> 5;
 
     // Logical block id: XCD-local, then (bh, split, m-block) with the m-block fastest. bh is
     // (batch, query head), or (batch, kv head) when the query heads of a GQA group are packed
@@ -463,7 +465,7 @@ struct FwdKernel {
     // (causal) rows that all precede the tile.
     auto active = [&](int t) { return wave_has_rows && !(p.causal && t * BN > wrow0 + ROWS - 1); };
 
-    if (STAGES == 1) {
+    if constexpr (STAGES == 1) {
       uint16_t* ks = smem;
       uint16_t* vs = smem + KTILE;
       u32x4 pkr[PASSES], pvr[PASSES];
@@ -491,7 +493,7 @@ struct FwdKernel {
           pv_schedule();
         }
       }
-    } else if (STAGES == 3) {
+    } else if constexpr (STAGES == 3) {
       // Software pipeline across KV tiles inside each wave. Step u starts with S_u = K_u Q^T and
       // its row max already computed, then
       //   (rare branch) lazy rescale for tile u
@@ -508,39 +510,38 @@ struct FwdKernel {
       uint16_t* vring = smem + RING * KT_ELEMS;
       const auto krs = make_rsrc(p.k + (int64_t)b * p.sk0 + (int64_t)hk * p.sk1, (uint32_t)p.N * (uint32_t)p.sk2 * 2u);
       const auto vrs = make_rsrc(p.v + (int64_t)b * p.sv0 + (int64_t)hk * p.sv1, (uint32_t)p.N * (uint32_t)p.sv2 * 2u);
-      // Byte offsets (within a tile) of the 16 bytes this lane moves for each block of this wave.
-      uint32_t koffs[NKW], voffs[NVW];
-#pragma unroll
-      for (int j = 0; j < NKW; ++j) {
-        const int blk = wave * NKW + j, jt = blk / DC, cc = blk % DC;
+      // Byte offset (within a tile) of the 16 bytes this lane moves for the first block of this
+      // wave. A wave's blocks are consecutive d chunks of one 32-key tile (K: +16 columns = +32
+      // bytes per block) or consecutive d tiles of one 16-key chunk (V: +32 columns = +64 bytes),
+      // so the other blocks differ by an immediate offset.
+      static_assert(DC % NKW == 0 && DTL % NVW == 0, "a wave's DMA blocks stay in one key group");
+      uint32_t koff, voff;
+      {
+        const int blk = wave * NKW, jt = blk / DC, cc = blk % DC;
         const uint32_t row = jt * 32 + (lane & 31), c0 = cc * 16 + 8 * (lane >> 5);
-        koffs[j] = (row * (uint32_t)p.sk2 + c0) * 2u;
+        koff = (row * (uint32_t)p.sk2 + c0) * 2u;
       }
-#pragma unroll
-      for (int j = 0; j < NVW; ++j) {
-        const int blk = wave * NVW + j, kc = blk / DTL, dt = blk % DTL;
+      {
+        const int blk = wave * NVW, kc = blk / DTL, dt = blk % DTL;
         const int m = lane & 31, half = lane >> 5;  // the lane pair (2m, 2m+1) of read `half`
         const uint32_t row = kc * 16 + 8 * half + 4 * (m >> 4) + ((m & 7) >> 1);
         const uint32_t c0 = dt * 32 + 16 * ((m >> 3) & 1) + 8 * (m & 1);
-        voffs[j] = (row * (uint32_t)p.sv2 + c0) * 2u;
+        voff = (row * (uint32_t)p.sv2 + c0) * 2u;
       }
-      // DMA destinations as LDS byte addresses from the wave index in a scalar register: M0 is
-      // then computed with scalar instructions only.
+      // DMA destinations as LDS byte addresses from the (scalar) wave index: M0 is computed with
+      // scalar instructions only.
       const uint32_t kring_lds = lds_address(smem), vring_lds = kring_lds + RING * KT_ELEMS * 2;
-      const int wave_u = __builtin_amdgcn_readfirstlane(wave);
       auto issue_k = [&](int u) {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
         const uint32_t slot = kring_lds + (uint32_t)(u % RING) * (KT_ELEMS * 2);
-#pragma unroll
-        for (int j = 0; j < NKW; ++j) buffer_load16_to_lds(krs, koffs[j] + toff, slot + (wave_u * NKW + j) * 1024);
+        buffer_load16_to_lds_blocks<NKW, 32>(krs, koff + toff, slot + wave * NKW * 1024);
       };
       auto issue_v = [&](int u) {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
         const uint32_t slot = vring_lds + (uint32_t)(u % RING) * (VT_ELEMS * 2);
-#pragma unroll
-        for (int j = 0; j < NVW; ++j) buffer_load16_to_lds(vrs, voffs[j] + toff, slot + (wave_u * NVW + j) * 1024);
+        buffer_load16_to_lds_blocks<NVW, 64>(vrs, voff + toff, slot + wave * NVW * 1024);
       };
       const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
       const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
