@@ -117,12 +117,13 @@ __device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
 // vmcnt retires in order, so the compiler's own vmcnt waits stay correct (they can only wait
 // longer when these loads are outstanding).
 // `lds_block` is the block's LDS byte address (lds_address of the __shared__ array plus a
-// wave-uniform offset), so M0 is computed with scalar instructions. IMM is added to byte_off by the
-// instruction's 12-bit offset field (the range check applies to the sum).
+// wave-uniform offset), so M0 is computed with scalar instructions. IMM is the instruction's 12-bit
+// offset field: the hardware adds it to the memory offset (byte_off) AND to the LDS address
+// (M0 + IMM + 16 * lane), so M0 is set to lds_block - IMM.
 template <int IMM = 0>
 __device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
   static_assert(IMM >= 0 && IMM < 4096, "12-bit immediate offset");
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_block);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_block - (uint32_t)IMM);
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen offset:%3 lds"
                :
                : "v"(byte_off), "s"(lds), "s"(rsrc), "n"(IMM)
