@@ -254,8 +254,11 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
     mp.so0 = p.so0; mp.so1 = p.so1; mp.so2 = p.so2;
     mp.sl0 = p.sl0; mp.sl1 = p.sl1; mp.sl2 = p.sl2;
     mp.B = a->B; mp.H = a->H; mp.M = a->M; mp.splits = splits;
+    // up to 16 splits per wave: decode rows (few rows, many splits) get 2 or 4 waves each
+    mp.waves_per_row = splits > 32 ? 4 : (splits > 16 ? 2 : 1);
     const int64_t rows = (int64_t)a->B * a->H * a->M;
-    const int64_t blocks = (rows + 3) / 4;
+    const int64_t rows_per_block = 4 / mp.waves_per_row;
+    const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
     if (blocks > 0x7fffffffLL) return fail(FA_EINVAL, "merge grid too large");
     void* margs[] = {&mp};
     err = hipLaunchKernel(me->fn, dim3((unsigned)blocks), dim3(256), margs, 0, s);

@@ -701,49 +701,110 @@ __global__ __launch_bounds__(WAVES * 64, (WAVES == 4 && RT == 1 && D <= 128) ? 2
   FwdKernel<Tag, D, WAVES, RT, BN, STAGES, SPLIT>::run(p);
 }
 
-// Merge of split-KV partials: one wave per query row.
+// Merge of split-KV partials. A query row's splits are shared by waves_per_row waves of the
+// workgroup (1, 2 or 4; decode rows merge tens of splits, and a wave waiting on one load per split
+// was latency-bound). Each wave computes the weights of its splits 64 at a time (lane s holds split
+// c + s), then takes its splits in batches of 16: one readlane of the weight and one vector load of
+// the partial row per split (lane l owns d = PL l .. PL l + PL - 1), all 16 loads in flight
+// together. The waves of a row add their partial sums through LDS.
+template <int PL>
+struct MergeVec;
+template <>
+struct MergeVec<1> { typedef float type; };
+template <>
+struct MergeVec<2> { typedef float type __attribute__((ext_vector_type(2))); };
+template <>
+struct MergeVec<4> { typedef floatx4 type; };
+
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   typedef DT<Tag> T;
-  constexpr int PER_LANE = D / 64 > 0 ? D / 64 : 1;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int PL = D / 64;
+  static_assert(D == 64 * PL && (PL == 1 || PL == 2 || PL == 4), "merge layout");
+  typedef typename MergeVec<PL>::type fvec;
+  constexpr int kBatch = 16;
+  __shared__ float part_acc[4][D];
+  __shared__ float part_sum[4];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpr = p.waves_per_row;
   const int64_t rows = (int64_t)p.B * p.H * p.M;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= rows) return;
-  const int64_t bh = row / p.M;
-  const int i = (int)(row % p.M);
+  const int64_t row = (int64_t)blockIdx.x * (4 / wpr) + wave / wpr;
+  const int part = wave % wpr;
+  const bool live = row < rows;  // no early return: the waves of a row meet at a barrier
   const int64_t split_stride = rows;  // rows per split
 
   constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.69314718055994530942f;
   float mx = FA_NEG_INF;
-  for (int s = lane; s < p.splits; s += 64) mx = fmaxf(mx, p.ws_lse[s * split_stride + row]);
+  if (live)
+    for (int s = lane; s < p.splits; s += 64) mx = fmaxf(mx, p.ws_lse[s * split_stride + row]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
 
-  float acc[PER_LANE];
+  float acc[PL];
 #pragma unroll
-  for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
-  float wsum = 0.f;
-  if (mx != FA_NEG_INF) {
-    for (int s = 0; s < p.splits; ++s) {
-      const float ls = p.ws_lse[s * split_stride + row];
-      const float w = fast_exp2((ls - mx) * kLog2e);  // 0 for an empty split (ls = -inf)
-      wsum += w;
-      const float* src = p.ws_o + (s * split_stride + row) * D;
+  for (int e = 0; e < PL; ++e) acc[e] = 0.f;
+  float wsum = 0.f;  // this lane's splits; summed over the wave below
+  const int per = (p.splits + wpr - 1) / wpr;
+  const int s_begin = min(part * per, p.splits), s_end = min(s_begin + per, p.splits);
+  if (live && mx != FA_NEG_INF) {
+    const float* src = p.ws_o + row * D + lane * PL;
+    for (int c = s_begin; c < s_end; c += 64) {
+      const int s_lane = c + lane;
+      const float ls = (s_lane < s_end) ? p.ws_lse[s_lane * split_stride + row] : FA_NEG_INF;
+      const float w_lane = fast_exp2((ls - mx) * kLog2e);  // 0 for empty or absent splits (ls = -inf)
+      wsum += w_lane;
+      const int cnt = min(64, s_end - c);
+      for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+        // indices past cnt re-read the last split (a valid address) with weight 0
+        fvec o[kBatch];
+        float w[kBatch];
 #pragma unroll
-      for (int e = 0; e < PER_LANE; ++e) {
-        const int d = lane + 64 * e;
-        if (d < D) acc[e] += w * src[d];
+        for (int u = 0; u < kBatch; ++u) {
+          const int j = min(j0 + u, cnt - 1);
+          w[u] = (j0 + u < cnt)
+                     ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_lane), j))
+                     : 0.f;
+          o[u] = *reinterpret_cast<const fvec*>(src + (int64_t)(c + j) * split_stride * D);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if constexpr (PL == 1) {
+            acc[0] += w[u] * o[u];
+          } else {
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[e] += w[u] * o[u][e];
+          }
+        }
       }
     }
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) wsum += __shfl_xor(wsum, off, 64);
+  if (wpr > 1) {
+#pragma unroll
+    for (int e = 0; e < PL; ++e) part_acc[wave][lane * PL + e] = acc[e];
+    if (lane == 0) part_sum[wave] = wsum;
+    __syncthreads();
+    if (part != 0 || !live) return;
+    for (int k = 1; k < wpr; ++k) {
+#pragma unroll
+      for (int e = 0; e < PL; ++e) acc[e] += part_acc[wave + k][lane * PL + e];
+      wsum += part_sum[wave + k];
+    }
+  } else if (!live) {
+    return;
+  }
+  const int64_t bh = row / p.M;
+  const int i = (int)(row % p.M);
   const float inv = (wsum > 0.f) ? 1.f / wsum : 0.f;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-  uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)h * p.so1 + (int64_t)i * p.so2;
+  uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)h * p.so1 + (int64_t)i * p.so2 + lane * PL;
+  if constexpr (PL == 1) {
+    orow[0] = T::from_float(acc[0] * inv);
+  } else {
 #pragma unroll
-  for (int e = 0; e < PER_LANE; ++e) {
-    const int d = lane + 64 * e;
-    if (d < D) orow[d] = T::from_float(acc[e] * inv);
+    for (int e = 0; e < PL; e += 2)
+      *reinterpret_cast<uint32_t*>(orow + e) = T::pack2(acc[e] * inv, acc[e + 1] * inv);
   }
   if (p.lse != nullptr && lane == 0)
     p.lse[(int64_t)b * p.sl0 + (int64_t)h * p.sl1 + (int64_t)i * p.sl2] =

@@ -41,6 +41,7 @@ struct MergeParams {
   int64_t so0, so1, so2;
   int64_t sl0, sl1, sl2;
   int32_t B, H, M, splits;
+  int32_t waves_per_row;  // 1, 2 or 4: the waves of a workgroup that share one row's splits
 };
 
 typedef void (*FwdKernelFn)(FwdParams);

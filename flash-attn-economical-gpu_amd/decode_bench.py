@@ -51,6 +51,32 @@ def _time(fn, warmup: int = 3, iters: int = 20) -> float:
     return statistics.median(times)
 
 
+def _time_graph(fn, iters: int = 20) -> tuple[float, torch.Tensor]:
+    """Median time of replaying one call captured in a HIP graph (torch.cuda.CUDAGraph): the GPU
+    time of the split and merge launches without the host's per-call launch cost, which dominates a
+    single decode step. Returns (ms, the graph's output tensor)."""
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times), out
+
+
 def run_case(label, B, H, Hkv, M, N, D, dtype, seed: int = 0) -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device="cpu").manual_seed(seed)
@@ -63,6 +89,8 @@ def run_case(label, B, H, Hkv, M, N, D, dtype, seed: int = 0) -> dict:
     torch.cuda.synchronize()
     err = (out.float() - ref.float()).abs().max().item()
     ms = _time(ours)
+    ms_graph, out_graph = _time_graph(ours)
+    graph_diff = (out_graph.float() - out.float()).abs().max().item()
     ms_torch = _time(lambda: F.scaled_dot_product_attention(q, k, v, scale=D ** -0.5, enable_gqa=True))
     elt = q.element_size()
     kv_bytes = 2 * B * Hkv * N * D * elt
@@ -73,11 +101,14 @@ def run_case(label, B, H, Hkv, M, N, D, dtype, seed: int = 0) -> dict:
         "ms": round(ms, 4), "ms_torch_sdpa": round(ms_torch, 4), "speedup_vs_torch": round(ms_torch / ms, 2),
         "algorithmic_bytes": io_bytes, "GBs": round(io_bytes / ms / 1e6, 1),
         "hbm_frac": round(io_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "TFLOPs": round(flops / ms / 1e9, 1),
+        "ms_graph": round(ms_graph, 4), "GBs_graph": round(io_bytes / ms_graph / 1e6, 1),
+        "hbm_frac_graph": round(io_bytes / ms_graph / 1e6 / HBM_PEAK_GBS, 4), "graph_vs_eager_max_abs": graph_diff,
         "max_abs_vs_torch": err,
     }
-    print(f"[decode] {label}: {ms:.4f} ms = {row['GBs']:.0f} GB/s ({100 * row['hbm_frac']:.1f}% of 8 TB/s), "
+    print(f"[decode] {label}: {ms:.4f} ms = {row['GBs']:.0f} GB/s ({100 * row['hbm_frac']:.1f}% of 8 TB/s); "
+          f"graph replay {ms_graph:.4f} ms = {row['GBs_graph']:.0f} GB/s ({100 * row['hbm_frac_graph']:.1f}%); "
           f"torch SDPA {ms_torch:.4f} ms ({row['speedup_vs_torch']:.2f}x), max|diff|={err:.2e}", flush=True)
-    del q, k, v, out, ref
+    del q, k, v, out, ref, out_graph
     torch.cuda.empty_cache()
     return row
 

@@ -57,6 +57,9 @@ DECODE = [
     ("w8_tile", 1, 16, 2, 9, 900, 128, BF16, (256, 64, 8, 3), 4),
     ("double_buffered", 2, 32, 8, 2, 1200, 128, F16, (128, 64, 4, 2), 8),
     ("group_exceeds_tile", 1, 16, 1, 9, 640, 64, F16, (128, 64, 4, 3), 4),  # 16*9 > 128: no packing
+    # more splits than a wave has lanes: the merge takes split weights 64 at a time; 36 splits empty
+    ("many_splits", 1, 8, 2, 1, 8192, 128, BF16, (128, 64, 4, 3), 100),
+    ("many_splits_d256", 1, 4, 4, 2, 4000, 256, F16, (128, 32, 4, 3), 70),
 ]
 
 
@@ -101,4 +104,37 @@ def test_decode_through_sdpa_entry(gpu, M):
     out = flash_atten.sdpa(qd, kd, vd, is_causal=False, scale=D ** -0.5, variant="sliced")
     torch.cuda.synchronize()
     o_ref, _ = oracle.attention(q, k, v, causal=False)
+    assert max_abs(out.float().cpu().numpy(), o_ref) <= ATOL[BF16]
+
+
+@pytest.mark.gpu
+def test_decode_step_replays_in_a_hip_graph(gpu):
+    """A decode step (split pass + merge pass, workspace from torch's allocator) captured in a HIP
+    graph replays correctly: between replays the query changes in place (eager work on the same
+    stream), and every replay must match an eager call on the new query."""
+    B, H, Hkv, M, N, D = 1, 32, 8, 1, 6000, 128
+    print("[decode] HIP graph capture and replays", flush=True)
+    q, k, v = make_qkv(9090, B, H, Hkv, M, N, D, BF16)
+    qd, kd, vd = (to_device(x, BF16, "cuda:0") for x in (q, k, v))
+
+    def step():
+        return flash_atten.sdpa(qd, kd, vd, is_causal=False, scale=D ** -0.5, variant="sliced")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    g = torch.Generator().manual_seed(5)
+    for rep in range(4):
+        qd.copy_(torch.randn(qd.shape, generator=g).to(BF16))
+        eager = step()
+        graph.replay()
+        torch.cuda.synchronize()
+        diff = (out.float() - eager.float()).abs().max().item()
+        assert diff == 0.0, (rep, diff)
+    o_ref, _ = oracle.attention(qd.float().cpu().numpy(), k, v, causal=False)
     assert max_abs(out.float().cpu().numpy(), o_ref) <= ATOL[BF16]
