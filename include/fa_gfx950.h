@@ -137,7 +137,9 @@ int32_t fa_fwd_pack_group(int32_t H, int32_t H_kv, int32_t M, int32_t causal, in
 int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile);
 
 /* C[M,N] (fp16, row stride ldc) = A[M,K] (fp16, lda) x B[K,N] (fp16, ldb), fp32 accumulation;
- * launches on `stream`. M, N, K must be multiples of the tile (mma.py:63-81 raises otherwise). */
+ * launches on `stream`. Partial tiles are masked: any M, with K % 8 == 0 and N % 4 == 0 (16-byte
+ * loads, 8-byte stores); lda and ldb multiples of 8, ldc of 4. (The reference needs multiples of
+ * the tile, mma.py:63-81; its selector, mma._select_2d_contiguous_config, keeps that rule.) */
 int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_t K,
              int64_t lda, int64_t ldb, int64_t ldc, const gemm_tile* tile, void* stream);
 
