@@ -72,6 +72,9 @@ struct GemmKernel {
   static_assert(BP >= 128 && QB >= 2, "B swizzle assumes rows of at least 128 bytes");
   static_assert(A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0, "slab must split evenly");
   static_assert(RING * SLAB_BYTES <= 160 * 1024, "LDS");
+  static constexpr int CP = BN * 2;                      // C tile row pitch in LDS (bytes)
+  static constexpr int CHS = CP / 16 < 16 ? CP / 16 : 16;  // swizzled 16-byte chunks per C row
+  static_assert(BM * CP <= RING * SLAB_BYTES, "the C tile is staged in the slab ring");
 
   __device__ static inline void compute(floatx16 (&acc)[TN][TM], const char* slab, const uint32_t (&aaddr)[KCH],
                                         const uint32_t (&baddr)[TN], int wm) {
@@ -229,23 +232,45 @@ struct GemmKernel {
         wait_vm_lds_barrier<0>();
     }
 
-    // C^T tile: lane holds row m = ...+col, columns n = 8*gq + 4*hh + 0..3 of each 32-col tile
-    // (N % 4 == 0, so each 4-column group is wholly inside or outside the matrix).
+    // C goes out through LDS (the ring is free after the last step's barrier): each lane holds 4
+    // consecutive columns of one row per 32x32 tile (C^T layout), which as direct 8-byte stores
+    // left C lines written in pieces; staged in LDS, each lane stores 16 contiguous bytes and 8
+    // lanes a full 128-byte line. LDS rows are XOR-swizzled in 16-byte chunks
+    // (chunk ^ (row & (CHS - 1))), so the 32 rows one write instruction touches spread over the banks.
+    char* ctile = smem;
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      const int m = m0 + (wm * TM + tm) * 32 + col;
-      if (m >= p.M) continue;
-      uint16_t* crow = p.c + (int64_t)m * p.ldc + n0;
+      const int r = (wm * TM + tm) * 32 + col;
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-          const int n = (wn * TN + tn) * 32 + 8 * gq + 4 * hh;
-          if (n0 + n >= p.N) continue;
-          u32x2 val = {DT<f16_t>::pack2(acc[tn][tm][4 * gq], acc[tn][tm][4 * gq + 1]),
-                       DT<f16_t>::pack2(acc[tn][tm][4 * gq + 2], acc[tn][tm][4 * gq + 3])};
-          *reinterpret_cast<u32x2*>(crow + n) = val;
+          const int cb = ((wn * TN + tn) * 32 + 8 * gq + 4 * hh) * 2;  // byte column in the tile row
+          const int phys = r * CP + ((((cb >> 4) ^ (r & (CHS - 1)))) << 4) + (cb & 15);
+          *reinterpret_cast<u32x2*>(ctile + phys) =
+              (u32x2){DT<f16_t>::pack2(acc[tn][tm][4 * gq], acc[tn][tm][4 * gq + 1]),
+                      DT<f16_t>::pack2(acc[tn][tm][4 * gq + 2], acc[tn][tm][4 * gq + 3])};
         }
+    }
+    __syncthreads();
+    // 16-byte global stores need C and its row stride 16-byte aligned (the ABI guarantees 8).
+    const bool c16 = ((reinterpret_cast<uintptr_t>(p.c) & 15) == 0) && ((p.ldc & 7) == 0);
+    constexpr int CHUNKS = BM * CP / 16;  // 16-byte chunks of the C tile
+    static_assert(CHUNKS % (WAVES * 64) == 0, "C tile chunks split evenly over the threads");
+#pragma unroll 4
+    for (int i = tid; i < CHUNKS; i += WAVES * 64) {
+      const int r = i / (CP / 16), c = i % (CP / 16);
+      const int m = m0 + r, n = n0 + c * 8;
+      if (m >= p.M || n >= p.N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ctile + r * CP + ((c ^ (r & (CHS - 1))) << 4));
+      uint16_t* dst = p.c + (int64_t)m * p.ldc + n;
+      if (c16 && n + 8 <= p.N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        // N % 4 == 0: the chunk's first 4 columns are in range, its last 4 only when n + 8 <= N
+        *reinterpret_cast<u32x2*>(dst) = (u32x2){v[0], v[1]};
+        if (n + 8 <= p.N) *reinterpret_cast<u32x2*>(dst + 4) = (u32x2){v[2], v[3]};
+      }
     }
   }
 };
