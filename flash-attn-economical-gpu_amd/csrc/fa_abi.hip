@@ -313,8 +313,11 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
   if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large");
   p.region_m = gemm_region_rows(p.tiles_m, p.tiles_n, e->block_m, e->block_n);
+  // Short K loops run the tile's shallow-ring kernel where one is built (more workgroups per CU).
+  const int slabs = (K + e->block_k - 1) / e->block_k;
+  const void* fn = (e->fn_shallow && slabs <= fa::kGemmShallowMaxSlabs) ? e->fn_shallow : e->fn;
   void* kargs[] = {&p};
-  hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0,
+  hipError_t err = hipLaunchKernel(fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0,
                                    static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(FA_EHIP, "gemm launch failed: %s", hipGetErrorString(err));
   return ok();

@@ -80,8 +80,13 @@ struct GemmParams {
 
 struct GemmKernelEntry {
   int32_t block_m, block_n, block_k, waves;
-  const void* fn;
+  const void* fn;          // default slab ring (as deep as fits in 128 KiB, up to 4)
+  const void* fn_shallow;  // shallow ring for short K (nullptr when it would be the same)
 };
+
+// K slabs up to which a tile's shallow-ring kernel is launched (more workgroups per CU beat a
+// deeper prefetch when the whole K loop is this short).
+constexpr int kGemmShallowMaxSlabs = 8;
 
 const GemmKernelEntry* gemm_registry(int* count);
 

@@ -44,7 +44,7 @@ __device__ inline u32x2 gemm_lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, bool SHALLOW = false>
 struct GemmKernel {
   static constexpr int WAVES = WM * WN;
   static constexpr int TM = BM / WM / 32;  // 32-row tiles per wave along M
@@ -60,9 +60,13 @@ struct GemmKernel {
   static constexpr int A_BYTES = BM * AP;
   static constexpr int B_BYTES = BK * BP;
   static constexpr int SLAB_BYTES = A_BYTES + B_BYTES;
-  // Slabs resident in LDS: as many as fit in 128 KiB, 2..4.
+  // Slabs resident in LDS: as many as fit in 128 KiB, 2..4. The SHALLOW variant keeps the fewest
+  // that still hold the staged C tile (at least 2): less LDS per workgroup, so more workgroups
+  // share a CU, which pays when K is only a few slabs deep (their latency is then the cost).
   static constexpr int RING_FIT = 131072 / SLAB_BYTES;
-  static constexpr int RING = RING_FIT > 4 ? 4 : (RING_FIT < 2 ? 2 : RING_FIT);
+  static constexpr int RING_DEEP = RING_FIT > 4 ? 4 : (RING_FIT < 2 ? 2 : RING_FIT);
+  static constexpr int RING_C = (BM * BN * 2 + SLAB_BYTES - 1) / SLAB_BYTES;
+  static constexpr int RING = SHALLOW ? (RING_C > 2 ? RING_C : 2) : RING_DEEP;
   static constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;  // DMA instructions per wave per slab
   static constexpr int B_PER_WAVE = B_BYTES / 1024 / WAVES;
   static constexpr int DMA_PER_SLAB = A_PER_WAVE + B_PER_WAVE;
@@ -280,8 +284,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(GemmParams p) {
   GemmKernel<BM, BN, BK, WM, WN>::run(p);
 }
 
-#define GEMM_ENTRY(BM, BN, BK, WM, WN) \
-  {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN>}
+template <int BM, int BN, int BK, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_f16_shallow_kernel(GemmParams p) {
+  GemmKernel<BM, BN, BK, WM, WN, true>::run(p);
+}
+
+// The shallow-ring kernel of a tile, or nullptr when its ring would be as deep as the default one.
+template <int BM, int BN, int BK, int WM, int WN>
+const void* gemm_shallow_fn() {
+  if constexpr (GemmKernel<BM, BN, BK, WM, WN, true>::RING < GemmKernel<BM, BN, BK, WM, WN>::RING)
+    return (const void*)&gemm_f16_shallow_kernel<BM, BN, BK, WM, WN>;
+  else
+    return nullptr;
+}
+
+#define GEMM_ENTRY(BM, BN, BK, WM, WN)                                                  \
+  {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN>,             \
+   gemm_shallow_fn<BM, BN, BK, WM, WN>()}
 
 static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(256, 256, 64, 2, 4),
