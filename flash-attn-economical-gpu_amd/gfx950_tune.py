@@ -40,23 +40,30 @@ FA_SWEEP = (
     + [("decode_bf16_gqa", torch.bfloat16, b, 32, 8, 1, n, 128, False, ("sliced",))
        for b, n in ((1, 8192), (1, 32768), (1, 131072), (8, 32768), (32, 8192))]
 )
-GEMM_SWEEP = [(n, n, n) for n in (1024, 2048, 4096, 8192, 16384)] + [(8192, 8192, 256), (1024, 1024, 256)]
+GEMM_SWEEP = ([(n, n, n) for n in (1024, 2048, 4096, 8192, 16384)]
+              + [(8192, 8192, 256), (1024, 1024, 256), (4096, 4096, 512)])
 GROUP_MS = (4, 8, 16)
 
 
-def _time(fn, warmup: int, iters: int) -> float:
+def _time(fn, warmup: int, iters: int, batch_ms: float = 1.0) -> float:
+    """Median per-launch time (ms) of back-to-back launches: each of `iters` samples times a batch
+    of launches lasting about `batch_ms`, so short kernels are ranked by their steady rate rather
+    than by one launch from an idle queue."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(iters):
+
+    def sample(n: int) -> float:
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        fn()
+        for _ in range(n):
+            fn()
         e.record()
         torch.cuda.synchronize()
-        times.append(s.elapsed_time(e))
-    return statistics.median(times)
+        return s.elapsed_time(e) / n
+
+    batch = max(1, min(64, round(batch_ms / max(sample(1), 1e-3))))
+    return statistics.median(sample(batch) for _ in range(iters))
 
 
 def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5, log=print) -> None:
@@ -136,6 +143,15 @@ def main(argv: list[str] | None = None) -> int:
         print("gfx950_tune.py needs a GPU", file=sys.stderr)
         return 1
     table = {"fa": {}, "gemm": {}}
+    if args.only is not None:
+        # a partial sweep keeps the other half of an existing table
+        try:
+            with open(args.out) as fh:
+                old = json.load(fh)
+            table = {"fa": old.get("fa", {}), "gemm": old.get("gemm", {})}
+        except (OSError, ValueError):
+            pass
+        table[args.only] = {}
     t0 = time.time()
     iters = 3 if args.quick else 5
     if args.only in (None, "fa"):
