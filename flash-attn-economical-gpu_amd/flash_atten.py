@@ -120,7 +120,9 @@ class _HipAttentionKernel:
         tile = _tile_for(self.variant, q.dtype, D, causal, B, H, M, N, kwargs)
         splits = kwargs.get("SPLITS")
         if splits is None:
-            splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n, H_kv=k.shape[1], causal=causal)
+            splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n, H_kv=k.shape[1], causal=causal,
+                                        resident_per_cu=cfgs.split_residency(q.dtype, D, tile.block_m, tile.block_n,
+                                                                             tile.waves, tile.stages))
         splits = int(splits)
         workspace = kwargs.get("workspace")
         need = hip_lib.workspace_bytes(B, H, M, D, splits)
@@ -210,7 +212,9 @@ def sdpa(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, is_caus
     workspace = None
     if variant_code == hip_lib.FA_VARIANT_SLICED:
         splits = cfgs.choose_splits(B, H, M, N, tile.block_m, tile.block_n, H_kv=key.shape[1],
-                                    causal=bool(is_causal))
+                                    causal=bool(is_causal),
+                                    resident_per_cu=cfgs.split_residency(query.dtype, D, tile.block_m, tile.block_n,
+                                                                         tile.waves, tile.stages))
         need = hip_lib.workspace_bytes(B, H, M, D, splits)
         if need:
             workspace = torch.empty(need, dtype=torch.uint8, device=query.device)

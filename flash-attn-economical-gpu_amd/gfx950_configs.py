@@ -76,9 +76,13 @@ GEMM_TILE_SPACE = [
 ]
 GEMM_DEFAULT_GROUP_M = 8
 
-# Workgroups wanted in flight before the sliced variant stops splitting KV (2 per CU).
-TARGET_WORKGROUPS = 512
+# The sliced variant splits KV until every CU holds as many workgroups as the kernel can keep
+# resident (RESIDENT_DEFAULT when its resources are unknown); splitting further only adds merge
+# traffic.
+NUM_CUS = 256
+RESIDENT_DEFAULT = 2
 MAX_SPLITS = 64
+LDS_PER_CU = 160 * 1024
 
 
 @dataclass(frozen=True)
@@ -209,19 +213,38 @@ def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M:
     return candidates[0]
 
 
+def split_residency(dtype, D: int, block_m: int, block_n: int, waves: int, stages: int) -> int:
+    """Workgroups of the sliced variant's split kernel one CU holds at once: the lower of the
+    register bound (waves per SIMD x 4 SIMDs / waves per workgroup) and the LDS bound, from the
+    compiler's resource table; RESIDENT_DEFAULT when the kernel is not in it."""
+    tile = hip_lib.FaTile(block_m, block_n, waves, stages, 2)
+    try:
+        res = hip_lib.compiled_resources().get(hip_lib.fwd_kernel_symbol(hip_lib.FA_VARIANT_SLICED, dtype, D, tile))
+    except (hip_lib.FaLibraryError, KeyError):
+        res = None
+    if not res:
+        return RESIDENT_DEFAULT
+    by_regs = max(1, int(res["Occupancy [waves/SIMD]"]) * 4 // waves)
+    lds = int(res["LDS Size [bytes/block]"])
+    by_lds = LDS_PER_CU // lds if lds else by_regs
+    return max(1, min(by_regs, by_lds))
+
+
 def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int, H_kv: int | None = None,
-                  causal: bool = False) -> int:
-    """KV splits for the sliced variant: split until ~TARGET_WORKGROUPS workgroups are in flight,
-    keeping at least two KV tiles per split. Split launches of decode shapes pack the query heads
-    of a GQA group into one tile (hip_lib.pack_group), so they count workgroups per kv head."""
+                  causal: bool = False, resident_per_cu: int = RESIDENT_DEFAULT) -> int:
+    """KV splits for the sliced variant: split until NUM_CUS x resident_per_cu workgroups (the
+    split kernel's resident capacity, split_residency) are in flight, keeping at least two KV tiles
+    per split. Split launches of decode shapes pack the query heads of a GQA group into one tile
+    (hip_lib.pack_group), so they count workgroups per kv head."""
     n_tiles = max(1, math.ceil(N / block_n))
     if n_tiles < 4:
         return 1
+    target = NUM_CUS * max(1, resident_per_cu)
 
     def splits_for(base: int) -> int:
-        if base >= TARGET_WORKGROUPS:
+        if base >= target:
             return 1
-        return max(1, min(math.ceil(TARGET_WORKGROUPS / base), n_tiles // 2, MAX_SPLITS))
+        return max(1, min(math.ceil(target / base), n_tiles // 2, MAX_SPLITS))
 
     H_kv = H if H_kv is None else H_kv
     group = hip_lib.pack_group(H, H_kv, M, causal, block_m, 2)

@@ -81,7 +81,10 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
                 splits = 1
                 ws = None
                 if variant == hip_lib.FA_VARIANT_SLICED:
-                    splits = cfgs.choose_splits(B, H, M, N, cand.block_m, cand.block_n, H_kv=Hkv, causal=causal)
+                    splits = cfgs.choose_splits(
+                        B, H, M, N, cand.block_m, cand.block_n, H_kv=Hkv, causal=causal,
+                        resident_per_cu=cfgs.split_residency(dtype, D, cand.block_m, cand.block_n, cand.waves,
+                                                             cand.stages))
                     need = hip_lib.workspace_bytes(B, H, M, D, splits)
                     ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
                 tile = cfgs.FaTileChoice(cand.block_m, cand.block_n, cand.waves, cand.stages, splits).to_c()

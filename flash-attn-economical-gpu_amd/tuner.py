@@ -521,8 +521,11 @@ class FlashAttentionBlockDNomaskTuner(FlashAttentionTuner):
         for config in out:
             config["BLOCK_DMODEL"] = int(self.tune_args.BLOCK_DMODEL or self.D)
             config["BLOCK_DMODEL_OUTER"] = int(self.tune_args.BLOCK_DMODEL_OUTER or self.D)
+            resident = cfgs.split_residency(dtype, self.D, int(config["BLOCK_M"]), int(config["BLOCK_N"]),
+                                            int(config["num_warps"]), int(config["num_stages"]))
             config["splits"] = cfgs.choose_splits(self.B, self.H, self.M, self.N, int(config["BLOCK_M"]),
-                                                  int(config["BLOCK_N"]), H_kv=self.H_kv, causal=self.causal)
+                                                  int(config["BLOCK_N"]), H_kv=self.H_kv, causal=self.causal,
+                                                  resident_per_cu=resident)
         return out
 
     def _build_candidate_launch(

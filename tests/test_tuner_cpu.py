@@ -312,6 +312,18 @@ def test_choose_splits():
     assert cfgs.choose_splits(1, 1, 64, 128, 256, 64) == 1  # too few KV tiles to split
 
 
+def test_split_residency_follows_the_resource_table():
+    # D=128 4-wave split kernels keep two workgroups per CU; the D=256 pipelined kernel (one wave
+    # per SIMD) and 8-wave kernels keep one
+    assert cfgs.split_residency(torch.float16, 128, 128, 64, 4, 3) == 2
+    assert cfgs.split_residency(torch.bfloat16, 256, 128, 32, 4, 3) == 1
+    assert cfgs.split_residency(torch.float16, 128, 256, 128, 8, 2) == 1
+    # B2 H16 M1024 D=256: 256 query tiles already fill every CU once, so no split (a split there
+    # only adds merge traffic); with two-per-CU residency the same grid would split in two
+    assert cfgs.choose_splits(2, 16, 1024, 1024, 128, 32, resident_per_cu=1) == 1
+    assert cfgs.choose_splits(2, 16, 1024, 1024, 128, 32, resident_per_cu=2) == 2
+
+
 def test_every_candidate_has_compiled_resources():
     for variant in (0, 1, 2):
         for dtype in (torch.float16, torch.bfloat16):
