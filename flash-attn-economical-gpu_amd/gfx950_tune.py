@@ -147,13 +147,15 @@ def main(argv: list[str] | None = None) -> int:
         return 1
     table = {"fa": {}, "gemm": {}}
     if args.only is not None:
-        # a partial sweep keeps the other half of an existing table
-        try:
-            with open(args.out) as fh:
-                old = json.load(fh)
+        # a partial sweep keeps the other half of the table at --out, or else of the installed one
+        for path in (args.out, str(cfgs.TUNE_TABLE_PATH)):
+            try:
+                with open(path) as fh:
+                    old = json.load(fh)
+            except (OSError, ValueError):
+                continue
             table = {"fa": old.get("fa", {}), "gemm": old.get("gemm", {})}
-        except (OSError, ValueError):
-            pass
+            break
         table[args.only] = {}
     t0 = time.time()
     iters = 3 if args.quick else 5
