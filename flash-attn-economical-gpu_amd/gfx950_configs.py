@@ -81,6 +81,8 @@ GEMM_DEFAULT_GROUP_M = 8
 # traffic.
 NUM_CUS = 256
 RESIDENT_DEFAULT = 2
+# Prefill-shaped sliced launches split only below this many workgroups (a quarter of the CUs).
+PREFILL_SPLIT_CUS = NUM_CUS // 4
 MAX_SPLITS = 64
 LDS_PER_CU = 160 * 1024
 
@@ -232,14 +234,19 @@ def split_residency(dtype, D: int, block_m: int, block_n: int, waves: int, stage
 
 def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int, H_kv: int | None = None,
                   causal: bool = False, resident_per_cu: int = RESIDENT_DEFAULT) -> int:
-    """KV splits for the sliced variant: split until NUM_CUS x resident_per_cu workgroups (the
-    split kernel's resident capacity, split_residency) are in flight, keeping at least two KV tiles
-    per split. Split launches of decode shapes pack the query heads of a GQA group into one tile
-    (hip_lib.pack_group), so they count workgroups per kv head."""
+    """KV splits for the sliced variant, keeping at least two KV tiles per split.
+
+    Decode-shaped grids (M < block_m: a few query rows per tile, K/V streaming dominates) split
+    until NUM_CUS x resident_per_cu workgroups (the split kernel's resident capacity,
+    split_residency) are in flight; their fp32 partials are a few rows each. Prefill-shaped grids
+    (full query tiles) write partials as large as the output and read them back in the merge, so
+    they split only when they would occupy fewer than PREFILL_SPLIT_CUS CUs. Split launches of
+    decode shapes pack the query heads of a GQA group into one tile (hip_lib.pack_group), so they
+    count workgroups per kv head."""
     n_tiles = max(1, math.ceil(N / block_n))
     if n_tiles < 4:
         return 1
-    target = NUM_CUS * max(1, resident_per_cu)
+    target = PREFILL_SPLIT_CUS if M >= block_m else NUM_CUS * max(1, resident_per_cu)
 
     def splits_for(base: int) -> int:
         if base >= target:

@@ -306,9 +306,15 @@ def test_filter_by_hints_relaxes_minimally():
 
 def test_choose_splits():
     assert cfgs.choose_splits(4, 32, 8192, 8192, 256, 64) == 1  # grid already fills the GPU
-    s = cfgs.choose_splits(1, 12, 4096, 4096, 256, 64)
-    assert 2 <= s <= cfgs.MAX_SPLITS
+    # prefill-shaped grids (full query tiles) split only below a quarter of the CUs
+    assert cfgs.choose_splits(1, 12, 4096, 4096, 256, 64) == 1  # 192 workgroups
+    assert cfgs.choose_splits(1, 28, 1024, 1024, 128, 64) == 1  # 224 workgroups
+    assert cfgs.choose_splits(1, 2, 256, 65536, 256, 64) == cfgs.PREFILL_SPLIT_CUS // 2
+    s = cfgs.choose_splits(1, 4, 512, 8192, 128, 64)              # 16 workgroups
+    assert s == cfgs.PREFILL_SPLIT_CUS // 16
+    # decode-shaped grids (a few rows per tile) split up to the resident capacity
     assert cfgs.choose_splits(1, 1, 1, 100000, 256, 64) == cfgs.MAX_SPLITS
+    assert cfgs.choose_splits(8, 32, 1, 32768, 128, 64) == 2  # 256 single-row tiles, 2 per CU
     assert cfgs.choose_splits(1, 1, 64, 128, 256, 64) == 1  # too few KV tiles to split
 
 
@@ -318,10 +324,10 @@ def test_split_residency_follows_the_resource_table():
     assert cfgs.split_residency(torch.float16, 128, 128, 64, 4, 3) == 2
     assert cfgs.split_residency(torch.bfloat16, 256, 128, 32, 4, 3) == 1
     assert cfgs.split_residency(torch.float16, 128, 256, 128, 8, 2) == 1
-    # B2 H16 M1024 D=256: 256 query tiles already fill every CU once, so no split (a split there
-    # only adds merge traffic); with two-per-CU residency the same grid would split in two
-    assert cfgs.choose_splits(2, 16, 1024, 1024, 128, 32, resident_per_cu=1) == 1
-    assert cfgs.choose_splits(2, 16, 1024, 1024, 128, 32, resident_per_cu=2) == 2
+    # decode shapes fill the resident capacity: 128 single-row tiles split in two when one split
+    # workgroup fits a CU, in four when two do
+    assert cfgs.choose_splits(1, 128, 1, 32768, 128, 32, resident_per_cu=1) == 2
+    assert cfgs.choose_splits(1, 128, 1, 32768, 128, 32, resident_per_cu=2) == 4
 
 
 def test_every_candidate_has_compiled_resources():
