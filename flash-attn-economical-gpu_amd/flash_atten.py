@@ -11,9 +11,11 @@ Same surface as the reference's `flash_atten.py` (flash_atten.py:364-389):
   * ``flash_attention(launch_spec)`` launches a spec built by the tuners and returns ``o`` or
     ``(o, lse)``; an unknown kernel name raises NameError (flash_atten.py:370-383).
 
-Variant meaning on gfx950: basic = single-buffered K/V LDS tiles; optimized = double-buffered
-K/V tiles (one barrier per KV tile); sliced = split-KV partials with an LSE merge pass (the
-reference's "sliced" split the head dimension instead; all three compute the same attention).
+Variant meaning on gfx950: basic = single-buffered K/V LDS tiles; optimized = the software-
+pipelined kernel (K/V rings filled by LDS-DMA, exp work of one tile under the MFMAs of the next;
+the double-buffered kernel where a tile asks for it); sliced = split-KV partials with an LSE merge
+pass (the reference's "sliced" split the head dimension instead; all three compute the same
+attention).
 """
 from __future__ import annotations
 

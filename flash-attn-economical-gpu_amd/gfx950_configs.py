@@ -14,6 +14,7 @@ Tile choice never changes results, only speed.
 """
 from __future__ import annotations
 
+import functools
 import json
 import math
 from dataclasses import dataclass
@@ -215,6 +216,7 @@ def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M:
     return candidates[0]
 
 
+@functools.lru_cache(maxsize=256)
 def split_residency(dtype, D: int, block_m: int, block_n: int, waves: int, stages: int) -> int:
     """Workgroups of the sliced variant's split kernel one CU holds at once: the lower of the
     register bound (waves per SIMD x 4 SIMDs / waves per workgroup) and the LDS bound, from the
