@@ -145,7 +145,7 @@ TRAFFIC_COMMAND = (
 )
 
 
-def _traffic_summarize(fetch_csv: str, write_csv: str) -> int:
+def _traffic_summarize(fetch_csv: str, write_csv: str, out_path: Path = TRAFFIC_FILE) -> int:
     """Write TRAFFIC_FILE from the two counter passes over --traffic-probe. FETCH_SIZE and WRITE_SIZE
     are KiB per dispatch (summed over the counter instances); each is scaled by the factor that
     makes the calibration copy read/write exactly its 256 MiB."""
@@ -190,7 +190,7 @@ def _traffic_summarize(fetch_csv: str, write_csv: str) -> int:
         out[key] = {"FETCH_SIZE_KiB": fk, "WRITE_SIZE_KiB": wk, "bytes_read": rd, "bytes_written": wr,
                     "bytes_per_launch": rd + wr, "algorithmic_bytes_per_launch": algo,
                     "ratio_to_algorithmic": round((rd + wr) / algo, 4)}
-    TRAFFIC_FILE.write_text(json.dumps(out, indent=2) + "\n")
+    Path(out_path).write_text(json.dumps(out, indent=2) + "\n")
     print(json.dumps(out, indent=2))
     return 0
 
@@ -217,7 +217,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one MI355X only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "the attention/GEMM path is single-GPU here: shard B*H (or KV splits) per GPU as DESIGN.md describes.",
+              "the attention/GEMM path is single-GPU here (it would shard B*H, or KV splits, one share per GPU).",
               file=sys.stderr)
         return 2
 
