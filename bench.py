@@ -35,6 +35,14 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_fa_b4h32n8192d128_gemm8192.json"
 SEED = 20260328  # the reference's constant (test_flash_atten.py:33)
 FA_SHAPE = dict(B=4, H=32, N=8192, D=128)
+# Attention workloads of the BASELINE configurations: the headline (default line) and, for
+# separate measurement, config 3's causal case at N=8192 and config 4's largest case.
+FA_CONFIGS = {
+    "headline": dict(B=4, H=32, N=8192, D=128, dtype="fp16", causal=False, variant="optimized", input_scale=1.0),
+    "fp16_d128_causal": dict(B=4, H=32, N=8192, D=128, dtype="fp16", causal=True, variant="optimized",
+                             input_scale=1.0),
+    "bf16_d256": dict(B=2, H=16, N=8192, D=256, dtype="bf16", causal=False, variant="sliced", input_scale=0.5),
+}
 GEMM_SHAPE = dict(M=8192, N=8192, K=8192)
 
 
@@ -203,7 +211,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--variant", default="optimized", choices=["basic", "optimized", "sliced"])
+    ap.add_argument("--fa-config", default="headline", choices=sorted(FA_CONFIGS),
+                    help="attention workload of the line (the default is the headline the metric names)")
+    ap.add_argument("--variant", default=None, choices=["basic", "optimized", "sliced"],
+                    help="attention variant (default: the workload's own)")
     ap.add_argument("--cpu-slices", type=int, default=4)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one 256 MiB copy (counter calibration), one attention forward and one GEMM, then exit "
@@ -238,18 +249,23 @@ def main() -> int:
     _log(f"device gfx{limits['gcn_arch']} CUs={limits['cu_count']} clock={limits['clock_khz'] / 1e6:.2f} GHz")
 
     # ---- attention forward ----------------------------------------------------------------------
-    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
+    fa_cfg = FA_CONFIGS[args.fa_config]
+    variant = args.variant or fa_cfg["variant"]
+    causal = fa_cfg["causal"]
+    fa_dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}[fa_cfg["dtype"]]
+    B, H, N, D = fa_cfg["B"], fa_cfg["H"], fa_cfg["N"], fa_cfg["D"]
     g = torch.Generator().manual_seed(SEED)
-    q, k, v = (torch.randn(B, H, N, D, generator=g, dtype=torch.float16).to(dev) for _ in range(3))
+    q, k, v = ((torch.randn(B, H, N, D, generator=g) * fa_cfg["input_scale"]).to(fa_dtype).to(dev) for _ in range(3))
     tuner_cls = {
         "basic": tuner.FlashAttentionTuner,
         "optimized": tuner.FlashAttentionOptimizeSharedMemTuner,
         "sliced": tuner.FlashAttentionBlockDNomaskTuner,
-    }[args.variant]
-    spec = tuner_cls(tuple(q.shape), tuple(k.shape), tuple(v.shape), q.element_size(), causal=False,
+    }[variant]
+    spec = tuner_cls(tuple(q.shape), tuple(k.shape), tuple(v.shape), q.element_size(), causal=causal,
                      return_lse=False).build_flash_attention_launch_spec(q, k, v)
-    fa_flops = 4.0 * B * H * N * N * D
-    _log(f"attention {args.variant}: tile {spec.kernel_kwargs['BLOCK_M']}x{spec.kernel_kwargs['BLOCK_N']} "
+    # the reference's FLOP count (test_flash_atten.py:234-240): causal counts N(N+1)/2 scores per (b, h)
+    fa_flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
+    _log(f"attention {args.fa_config} {variant}: tile {spec.kernel_kwargs['BLOCK_M']}x{spec.kernel_kwargs['BLOCK_N']} "
          f"waves={spec.kernel_kwargs['num_warps']} stages={spec.kernel_kwargs['num_stages']}")
     total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup)
     fa_launch_ms = statistics.mean(per)
@@ -266,10 +282,13 @@ def main() -> int:
     qs = q.reshape(B * H, N, D)[bh, m].float()
     ks = k.reshape(B * H, N, D)[bh].float()
     vs = v.reshape(B * H, N, D)[bh].float()
-    p = torch.softmax(torch.einsum("rd,rnd->rn", qs.to(dev), ks) * D ** -0.5, dim=-1)
+    sc = torch.einsum("rd,rnd->rn", qs.to(dev), ks) * D ** -0.5
+    if causal:  # top-left: row m sees keys j <= m
+        sc = sc.masked_fill(torch.arange(N, device=dev)[None, :] > m.to(dev)[:, None], float("-inf"))
+    p = torch.softmax(sc, dim=-1)
     ref = torch.einsum("rn,rnd->rd", p, vs)
     fa_err = (o.reshape(B * H, N, D)[bh, m].float() - ref).abs().max().item()
-    del q, k, v, spec, o, qs, ks, vs, p, ref
+    del q, k, v, spec, o, qs, ks, vs, sc, p, ref
     torch.cuda.empty_cache()
 
     # ---- GEMM ---------------------------------------------------------------------------------------
@@ -305,7 +324,9 @@ def main() -> int:
     if TRAFFIC_FILE.exists():
         try:
             recorded = json.loads(TRAFFIC_FILE.read_text())
-            traffic = recorded.get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
+            # the counter passes cover the headline launch only
+            if args.fa_config == "headline" and variant == "optimized":
+                traffic = recorded.get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
             gemm_traffic = recorded.get("gemm_f16_8192cube", {}).get("bytes_per_launch")
         except (ValueError, OSError):
             traffic = gemm_traffic = None
@@ -321,10 +342,11 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic (torch.randn fp16, seed 20260328)",
-        "config": {"workload": f"FlashAttention forward, {args.variant} variant, non-causal, sm_scale=1/sqrt(D)",
-                   "B": B, "H": H, "N": N, "D": D, "causal": False},
+        "dtype": fa_cfg["dtype"],
+        "data": (f"synthetic (torch.randn x {fa_cfg['input_scale']} rounded to {fa_cfg['dtype']}, seed 20260328)"),
+        "config": {"workload": (f"FlashAttention forward, {variant} variant, {'causal' if causal else 'non-causal'}, "
+                                f"sm_scale=1/sqrt(D)"),
+                   "B": B, "H": H, "N": N, "D": D, "causal": causal},
         "mfma_peak_frac": round(fa_tflops / PEAK_FP16_TFLOPS, 4),
         "roofline": {
             "bound": "mfma",
