@@ -139,7 +139,10 @@ int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* t
 /* C[M,N] (fp16, row stride ldc) = A[M,K] (fp16, lda) x B[K,N] (fp16, ldb), fp32 accumulation;
  * launches on `stream`. Partial tiles are masked: any M, with K % 8 == 0 and N % 4 == 0 (16-byte
  * loads, 8-byte stores); lda and ldb multiples of 8, ldc of 4. (The reference needs multiples of
- * the tile, mma.py:63-81; its selector, mma._select_2d_contiguous_config, keeps that rule.) */
+ * the tile, mma.py:63-81; its selector, mma._select_2d_contiguous_config, keeps that rule.)
+ * When K spans at most 8 slabs (K <= 8 * block_k) the tile's shallow-ring kernel runs (two LDS
+ * slabs, more workgroups per CU), where one is built; fa_kernel_resources reports the default
+ * (deep-ring) kernel of the tile. */
 int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_t K,
              int64_t lda, int64_t ldb, int64_t ldc, const gemm_tile* tile, void* stream);
 
