@@ -319,6 +319,21 @@ struct FwdKernel {
   static_assert(STAGES != 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
 
   __device__ static inline void qk_fm(STile& s, const u32x4 (&qf)[RT][DC], const uint16_t* kslot_lane) {
+    if constexpr (JT * RT == 1) {
+      // A single score tile (D = 256 with 32-key tiles) would be one chain of DC dependent MFMAs:
+      // run the even and odd d chunks as two independent chains and add them (+1.5% at D = 256).
+      floatx16 s0 = {}, s1 = {};
+#pragma unroll
+      for (int cc = 0; cc < DC; cc += 2) {
+        const u32x4 k0 = *reinterpret_cast<const u32x4*>(kslot_lane + cc * 512);
+        const u32x4 k1 = *reinterpret_cast<const u32x4*>(kslot_lane + (cc + 1) * 512);
+        s0 = T::mfma32(k0, qf[0][cc], s0);
+        s1 = T::mfma32(k1, qf[0][cc + 1], s1);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[0][0][r] = s0[r] + s1[r];
+      return;
+    }
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt)
 #pragma unroll
