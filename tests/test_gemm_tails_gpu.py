@@ -1,4 +1,4 @@
-"""GEMM shapes no tile divides (SURVEY (f)4 tails): the gfx950 kernel masks partial tiles in M, N
+"""GEMM shapes no tile divides (tails): the gfx950 kernel masks partial tiles in M, N
 and K (K % 8 == 0, N % 4 == 0). Checked against the exact oracle, with NaN in the row padding of A
 (past K) and B (past N) to show those elements never reach valid outputs, and a sentinel in C's
 padding to show nothing is stored outside [M, N)."""
