@@ -28,7 +28,7 @@ import hip_lib
 VARIANTS = {"basic": hip_lib.FA_VARIANT_BASIC, "optimized": hip_lib.FA_VARIANT_OPT,
             "sliced": hip_lib.FA_VARIANT_SLICED}
 
-# (name, dtype, B, H, H_kv, M, N, D, causal, variants) -- the BASELINE.json configurations, plus
+# (name, dtype, B, H, H_kv, M, N, D, causal, variants) -- the benchmark configurations, plus
 # decode shapes (a few query rows against a long KV cache) for the sliced variant
 FA_SWEEP = (
     [("fp16_d128", torch.float16, 4, 32, 32, n, n, 128, c, ("basic", "optimized", "sliced"))

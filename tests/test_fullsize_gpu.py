@@ -1,4 +1,5 @@
-"""BASELINE.json configurations at full size (GPU): sampled rows against the oracle plus
+"""The benchmark configurations at full size (GPU; fp16 B4 H32 N8192 D128, bf16 B2 H16 D256, the
+GQA 12:2 prefill, GEMM 1024..16384 squares): sampled rows against the oracle plus
 size-independent properties (first causal row copies V[0]; native GQA equals the expanded
 computation bit for bit; KV-split invariance; finite outputs), and the 8192^3 GEMM against an fp32
 product and sampled exact entries."""
