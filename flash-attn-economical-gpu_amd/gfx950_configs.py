@@ -234,6 +234,7 @@ def split_residency(dtype, D: int, block_m: int, block_n: int, waves: int, stage
     return max(1, min(by_regs, by_lds))
 
 
+@functools.lru_cache(maxsize=4096)
 def choose_splits(B: int, H: int, M: int, N: int, block_m: int, block_n: int, H_kv: int | None = None,
                   causal: bool = False, resident_per_cu: int = RESIDENT_DEFAULT) -> int:
     """KV splits for the sliced variant, keeping at least two KV tiles per split.

@@ -8,6 +8,7 @@ built for another ABI, every entry point raises RuntimeError.
 from __future__ import annotations
 
 import ctypes
+import functools
 import json
 import threading
 from pathlib import Path
@@ -191,22 +192,34 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise FaUnsupportedError(f"dtype {dtype} is not supported (float16, bfloat16)") from None
 
 
+# torch's raw current-stream query (what its own generated launchers call) skips building a Stream
+# object: a few microseconds per launch, which single-sequence decode steps pay on the host.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_I64x4 = ctypes.c_int64 * 4
+
+
 def _strides4(t: torch.Tensor):
-    return (ctypes.c_int64 * 4)(*[int(s) for s in t.stride()])
+    return _I64x4(*t.stride())
 
 
 def make_tile(block_m: int, block_n: int, waves: int, stages: int, splits: int = 1) -> FaTile:
     return FaTile(int(block_m), int(block_n), int(waves), int(stages), int(splits))
 
 
+@functools.lru_cache(maxsize=4096)
 def workspace_bytes(B: int, H: int, M: int, D: int, splits: int) -> int:
     return int(load().fa_fwd_workspace_bytes(B, H, M, D, splits))
 
 
+@functools.lru_cache(maxsize=4096)
 def pack_group(H: int, H_kv: int, M: int, causal: bool, block_m: int, splits: int) -> int:
     """Query heads fa_fwd packs into one tile's rows (1 = none); see fa_fwd_pack_group."""
     return int(load().fa_fwd_pack_group(H, H_kv, M, int(bool(causal)), block_m, splits))
