@@ -51,10 +51,11 @@ def _time(fn, warmup: int = 3, iters: int = 20) -> float:
     return statistics.median(times)
 
 
-def _time_graph(fn, iters: int = 20) -> tuple[float, torch.Tensor]:
-    """Median time of replaying one call captured in a HIP graph (torch.cuda.CUDAGraph): the GPU
-    time of the split and merge launches without the host's per-call launch cost, which dominates a
-    single decode step. Returns (ms, the graph's output tensor)."""
+def _time_graph(fn, iters: int = 20, batch: int = 20) -> tuple[float, torch.Tensor]:
+    """Per-step time of replaying one call captured in a HIP graph (torch.cuda.CUDAGraph), as a
+    decode loop runs it: `batch` back-to-back replays between two events, median over `iters`
+    such samples. This is the GPU time of the split and merge launches without the host's per-call
+    launch cost, which dominates a single eager decode step. Returns (ms, the graph's output)."""
     side = torch.cuda.Stream()  # default priority
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -70,10 +71,11 @@ def _time_graph(fn, iters: int = 20) -> tuple[float, torch.Tensor]:
     for _ in range(iters):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        graph.replay()
+        for _ in range(batch):
+            graph.replay()
         e.record()
         torch.cuda.synchronize()
-        times.append(s.elapsed_time(e))
+        times.append(s.elapsed_time(e) / batch)
     return statistics.median(times), out
 
 
