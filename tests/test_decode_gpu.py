@@ -28,8 +28,9 @@ def test_pack_rule():
     assert hip_lib.pack_group(12, 2, 1, False, 128, 16) == 6
     # the split count then targets the packed grid: one workgroup per (batch, kv head, split)
     s = cfgs.choose_splits(1, 32, 1, 32768, 128, 64, H_kv=8)
-    assert s == cfgs.MAX_SPLITS
+    assert s == 64  # 8 packed tiles x 64 splits = 512 workgroups, two per CU
     assert cfgs.choose_splits(1, 32, 1, 32768, 128, 64, H_kv=32) < s
+    assert cfgs.choose_splits(1, 12, 1, 32768, 128, 64, H_kv=2) == cfgs.MAX_SPLITS == 128
 
 
 def _run(q, k, v, *, dtype, tile, splits, causal=False, lse=True):
