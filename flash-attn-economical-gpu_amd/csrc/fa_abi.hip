@@ -106,6 +106,29 @@ const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_til
   return e;
 }
 
+// Does the pipelined (stages=3) kernel's addressing hold for this launch? It reads one (batch,
+// kv-head) row range [0, N + block_n) of K and V with 32-bit byte offsets, and its tail check needs
+// whole rows (row stride >= D).
+bool pipelined_fits(const fa_fwd_args* a, int block_n) {
+  const int64_t stride = a->k_stride[2] > a->v_stride[2] ? a->k_stride[2] : a->v_stride[2];
+  const int64_t span = ((int64_t)a->N + block_n) * 2 * stride;
+  return span <= 0xffffffffLL && a->k_stride[2] >= a->D && a->v_stride[2] >= a->D;
+}
+
+// The double-buffered kernel that replaces a pipelined one when pipelined_fits() fails: same
+// dtype, D, waves, rows per wave and split, the same block_n if built, else 64 keys.
+const fa::FaKernelEntry* double_buffered_fallback(const fa::FaKernelEntry* e) {
+  const fa::FaKernelEntry* fb = find_fwd(2, e->dtype, e->D, e->waves, e->rows_per_wave, e->block_n, e->split);
+  if (fb == nullptr) fb = find_fwd(2, e->dtype, e->D, e->waves, e->rows_per_wave, 64, e->split);
+  return fb;
+}
+
+const fa::KernelResourceRow* find_resource_row(const char* symbol) {
+  for (int i = 0; i < fa::kKernelResourceRowCount; ++i)
+    if (std::strcmp(fa::kKernelResourceRows[i].symbol, symbol) == 0) return &fa::kKernelResourceRows[i];
+  return nullptr;
+}
+
 // GEMM tile regions per XCD: the split of the tile grid into region_m x (8 / region_m) equal
 // rectangles whose A + B panel footprint (rows * block_m + columns * block_n) is smallest, or 0
 // (flat grouped order) when no split divides the grid.
@@ -154,11 +177,13 @@ int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* t
   const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
   if (e == nullptr) return code;
   if (split && find_merge(dtype, D) == nullptr) return fail(FA_ENOTSUP, "no merge kernel for D=%d", D);
+  if (e->stages == 3 && double_buffered_fallback(e) == nullptr)
+    return fail(FA_ENOTSUP, "pipelined tile without a double-buffered fallback for D=%d", D);
   return ok();
 }
 
-int fa_fwd(const fa_fwd_args* a, void* stream) {
-  if (a == nullptr) return fail(FA_EINVAL, "null argument block");
+// The body of fa_fwd: the split-KV workspace comes in as (ws, ws_bytes).
+static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
   bool split = false;
   int code = FA_OK;
   const fa::FaKernelEntry* e = resolve_fwd(a->variant, a->dtype, a->D, &a->tile, &split, &code);
@@ -179,7 +204,16 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
   if (!std::isfinite(a->sm_scale) || a->sm_scale <= 0.f)
     return fail(FA_EINVAL, "sm_scale must be positive and finite, got %g", (double)a->sm_scale);
 
-  const int bm = a->tile.block_m, bn = a->tile.block_n;
+  if (e->stages == 3 && !pipelined_fits(a, e->block_n)) {
+    // The pipelined kernel addresses one (batch, kv-head) row range [0, N + block_n) of K and V
+    // with 32-bit byte offsets and relies on whole rows for its tail check: run the
+    // double-buffered kernel of the same rows per workgroup instead (same block_n where it is
+    // built, else the 64-key tile: the D = 256 pipelined tile has 32 keys).
+    const fa::FaKernelEntry* fb = double_buffered_fallback(e);
+    if (fb == nullptr) return fail(FA_ENOTSUP, "no double-buffered fallback for the pipelined attention tile");
+    e = fb;
+  }
+  const int bm = a->tile.block_m, bn = e->block_n;
   const int splits = a->tile.splits < 1 ? 1 : a->tile.splits;
   // Decode shapes: when every query row of a GQA group fits in one tile (non-causal), the group's
   // query heads share the tile's rows, so each workgroup reads its kv head's K/V once for all of
@@ -220,24 +254,13 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
     me = find_merge(a->dtype, a->D);
     if (me == nullptr) return fail(FA_ENOTSUP, "no merge kernel for D=%d", a->D);
     const int64_t need = fa_fwd_workspace_bytes(a->B, a->H, a->M, a->D, splits);
-    if (a->workspace == nullptr || a->workspace_bytes < need)
+    if (ws == nullptr || ws_bytes < need)
       return fail(FA_EWORKSPACE, "split-KV workspace of %lld bytes needed, got %lld", (long long)need,
-                  (long long)a->workspace_bytes);
-    if (!aligned16(a->workspace)) return fail(FA_EINVAL, "workspace must be 16-byte aligned");
+                  (long long)ws_bytes);
+    if (!aligned16(ws)) return fail(FA_EINVAL, "workspace must be 16-byte aligned");
     const int64_t rows = (int64_t)splits * a->B * a->H * a->M;
-    p.ws_o = static_cast<float*>(a->workspace);
-    p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + ((rows * a->D * 4 + 255) & ~(int64_t)255));
-  }
-
-  if (e->stages == 3) {
-    // The pipelined kernel addresses one (batch, kv-head) row range [0, N + block_n) of K and V
-    // with 32-bit byte offsets and relies on whole rows for its tail check: fall back to the
-    // double-buffered kernel of the same tile when that does not hold.
-    const int64_t span = ((int64_t)a->N + bn) * 2 * (a->k_stride[2] > a->v_stride[2] ? a->k_stride[2] : a->v_stride[2]);
-    if (span > 0xffffffffLL || a->k_stride[2] < a->D || a->v_stride[2] < a->D) {
-      e = find_fwd(2, a->dtype, a->D, e->waves, e->rows_per_wave, e->block_n, e->split);
-      if (e == nullptr) return fail(FA_ENOTSUP, "no double-buffered fallback for the pipelined attention tile");
-    }
+    p.ws_o = static_cast<float*>(ws);
+    p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(ws) + ((rows * a->D * 4 + 255) & ~(int64_t)255));
   }
 
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -265,6 +288,11 @@ int fa_fwd(const fa_fwd_args* a, void* stream) {
     if (err != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(err));
   }
   return ok();
+}
+
+int fa_fwd(const fa_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(FA_EINVAL, "null argument block");
+  return launch_fwd(a, a->workspace, a->workspace_bytes, stream);
 }
 
 int gemm_f16_supported(const gemm_tile* tile) {
@@ -327,6 +355,7 @@ int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, c
                         const gemm_tile* gtile, fa_resources* out) {
   if (out == nullptr) return fail(FA_EINVAL, "null output");
   const void* fn = nullptr;
+  const char* symbol = nullptr;
   int threads = 0;
   if (op == 0) {
     bool split = false;
@@ -334,27 +363,32 @@ int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, c
     const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
     if (e == nullptr) return code;
     fn = e->fn;
+    symbol = e->symbol;
     threads = e->waves * 64;
   } else if (op == 1) {
     if (gtile == nullptr) return fail(FA_EINVAL, "null gemm tile");
     const fa::GemmKernelEntry* e = find_gemm(gtile);
     if (e == nullptr) return fail(FA_ENOTSUP, "gemm tile not built");
     fn = e->fn;
+    symbol = e->symbol;
     threads = e->waves * 64;
   } else {
     return fail(FA_EINVAL, "unknown op %d", op);
   }
+  const fa::KernelResourceRow* row = find_resource_row(symbol);
+  if (row == nullptr) return fail(FA_ENOTSUP, "no compiler resource row for %s (stale build)", symbol);
   hipFuncAttributes attr;
   std::memset(&attr, 0, sizeof(attr));
   hipError_t err = hipFuncGetAttributes(&attr, fn);
   if (err != hipSuccess) return fail(FA_EHIP, "hipFuncGetAttributes failed: %s", hipGetErrorString(err));
-  out->vgprs = attr.numRegs;
-  out->agprs = -1;
-  out->sgprs = -1;
+  out->vgprs = row->vgprs;
+  out->agprs = row->agprs;
+  out->sgprs = row->sgprs;
   out->lds_bytes = (int32_t)attr.sharedSizeBytes;
-  out->scratch_bytes = (int32_t)attr.localSizeBytes;
+  out->scratch_bytes = row->scratch_bytes;
   out->threads = threads;
   out->max_threads = attr.maxThreadsPerBlock;
+  out->occupancy = row->occupancy;
   return ok();
 }
 

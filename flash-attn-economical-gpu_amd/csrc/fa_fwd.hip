@@ -829,8 +829,16 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
 // ---------------------------------------------------------------------------------------------
 // Registry of built instantiations.
 
-#define FA_ENTRY(TAG, DTYPE, D, W, RT, BN, ST, SP) \
-  {ST, DTYPE, D, W, 32 * RT, BN, SP, (const void*)&fa_fwd_kernel<TAG, D, W, RT, BN, ST, (SP != 0)>}
+// Itanium-mangled names of the instantiations (arguments are literal tokens, so # spells them).
+#define FA_SYM_TAG_f16_t "5f16_t"
+#define FA_SYM_TAG_bf16_t "6bf16_t"
+#define FA_SYMBOL(TAG, D, W, RT, BN, ST, SP)                                                          \
+  "_ZN2fa13fa_fwd_kernelINS_" FA_SYM_TAG_##TAG "ELi" #D "ELi" #W "ELi" #RT "ELi" #BN "ELi" #ST "ELb" #SP \
+  "EEEvNS_9FwdParamsE"
+
+#define FA_ENTRY(TAG, DTYPE, D, W, RT, BN, ST, SP)                                         \
+  {ST, DTYPE, D, W, 32 * RT, BN, SP, (const void*)&fa_fwd_kernel<TAG, D, W, RT, BN, ST, (SP != 0)>, \
+   FA_SYMBOL(TAG, D, W, RT, BN, ST, SP)}
 
 #define FA_ENTRIES_D(TAG, DTYPE, D)                         \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 1, 0),                  \

@@ -300,7 +300,8 @@ const void* gemm_shallow_fn() {
 
 #define GEMM_ENTRY(BM, BN, BK, WM, WN)                                                  \
   {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN>,             \
-   gemm_shallow_fn<BM, BN, BK, WM, WN>()}
+   gemm_shallow_fn<BM, BN, BK, WM, WN>(),                                               \
+   "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "EEEvNS_10GemmParamsE"}
 
 static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(256, 256, 64, 2, 4),

@@ -18,7 +18,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libfa_gfx950.so"
 RESOURCES_PATH = HERE / "kernel_resources.json"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FA_OK, FA_EINVAL, FA_ENOTSUP, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
 FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1
@@ -84,6 +84,7 @@ class FaResources(ctypes.Structure):
         ("scratch_bytes", ctypes.c_int32),
         ("threads", ctypes.c_int32),
         ("max_threads", ctypes.c_int32),
+        ("occupancy", ctypes.c_int32),
     ]
 
 
@@ -229,21 +230,7 @@ def fa_fwd_supported(variant: int, dtype: torch.dtype, D: int, tile: FaTile) -> 
     return load().fa_fwd_supported(variant, dtype_code(dtype), D, ctypes.byref(tile)) == FA_OK
 
 
-def fa_fwd(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    o: torch.Tensor,
-    lse: torch.Tensor | None,
-    *,
-    sm_scale: float,
-    causal: bool,
-    variant: int,
-    tile: FaTile,
-    workspace: torch.Tensor | None = None,
-) -> None:
-    """Launch one attention forward: o (and lse) are written in place on the current stream."""
-    lib = load()
+def _fwd_args(q, k, v, o, lse, *, sm_scale, causal, variant, tile, workspace) -> FaFwdArgs:
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
         if t.dim() != 4:
             raise ValueError(f"{name} must be 4-D [batch, heads, seq, head_dim], got {tuple(t.shape)}")
@@ -275,6 +262,26 @@ def fa_fwd(
     args.causal = 1 if causal else 0
     args.variant = int(variant)
     args.tile = tile
+    return args
+
+
+def fa_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor | None,
+    *,
+    sm_scale: float,
+    causal: bool,
+    variant: int,
+    tile: FaTile,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Launch one attention forward: o (and lse) are written in place on the current stream."""
+    lib = load()
+    args = _fwd_args(q, k, v, o, lse, sm_scale=sm_scale, causal=causal, variant=variant, tile=tile,
+                     workspace=workspace)
     check(lib.fa_fwd(ctypes.byref(args), _stream_ptr(q.device)), "fa_fwd")
 
 
@@ -303,7 +310,8 @@ def gemm_supported(tile: GemmTile) -> bool:
 
 def kernel_resources_live(op: int, *, variant: int = 0, dtype: torch.dtype = torch.float16, D: int = 0,
                           tile: FaTile | None = None, gtile: GemmTile | None = None) -> dict[str, int]:
-    """Resources of one built kernel via hipFuncGetAttributes (needs a GPU)."""
+    """Resources of one built kernel (needs a GPU): registers, scratch and occupancy from the
+    compiler's table linked into the library, LDS and the workgroup limit from the loaded kernel."""
     out = FaResources()
     code = load().fa_kernel_resources(
         op, variant, dtype_code(dtype), D,

@@ -98,13 +98,22 @@ def _select_2d_contiguous_config(m: int, n: int, k: int) -> tuple[int, int, int,
 
 def matmul(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """C = A @ B through the gfx950 kernel (convenience entry). Unlike the reference selector it
-    accepts shapes no tile divides (K % 8 == 0 and N % 4 == 0; partial tiles are masked)."""
+    accepts shapes no tile divides (K % 8 == 0 and N % 4 == 0; partial tiles are masked). The
+    kernel reads B rows in 16-byte chunks, so B's row pitch must be a multiple of 8 elements: when
+    N % 8 == 4, B is first copied into rows of N + 4 elements (its last 4 columns are never
+    stored to C)."""
     a = a.contiguous()
     b = b.contiguous()
     M, K = a.shape
     _, N = b.shape
     c = torch.empty((M, N), device=a.device, dtype=torch.float16) if out is None else out
     bm, bn, bk, waves, group_m = cfgs.choose_gemm_tile_any(M, N, K)
+    if N % 8:
+        pitch = N + (-N) % 8
+        b_rows = torch.zeros((K, pitch), device=b.device, dtype=b.dtype)
+        b_rows[:, :N].copy_(b)
+        hip_lib.gemm_f16(a, b_rows[:, :N], c, hip_lib.GemmTile(bm, bn, bk, waves, group_m))
+        return c
     _matmul_contiguous_kernel[(-(-M // bm) * -(-N // bn),)](
         a, b, c, M, N, K, BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=group_m,
         USE_CACHE_EVICTION_HINTS=_supports_contiguous_cache_eviction_hints(a.device),

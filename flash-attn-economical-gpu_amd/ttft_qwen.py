@@ -8,7 +8,10 @@ Modelled on the reference's TTFT benchmark (paths relative to the reference repo
     ttft.py:203-215); bf16 and fp16 are accepted (the reference accepts fp16 only, ttft.py:172-173).
   * Prefill call: model(input_ids, use_cache=True, logits_to_keep=1) (ttft.py:401-408).
   * Verification: final-token logits against torch's own scaled_dot_product_attention,
-    allclose(rtol=atol=0.1) plus argmax agreement (ttft.py:415-446).
+    allclose(rtol=atol=0.1) plus argmax agreement (ttft.py:415-446). That is the pass rule of
+    main()'s exit status, as the reference raises on it (ttft.py:441-442). Reported beside it: the
+    same comparison between two of torch's own SDPA backends (default vs math), the deviation any
+    correct bf16 attention shows through 28 layers of random weights.
   * Timing: CUDA-event-timed prefills after warm-up (ttft.py:449-480).
 The model is built locally from the architecture numbers (28 layers, hidden 1536, 12 query / 2 KV
 heads of dim 128, SwiGLU 8960, RoPE base 1e6, RMSNorm, vocab 151936) with seeded random weights:
@@ -23,7 +26,7 @@ import contextlib
 import json
 import statistics
 import sys
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Iterator
 
 import torch
@@ -49,6 +52,14 @@ QWEN25_1P5B = dict(
 @dataclass
 class BackendUseStats:
     calls: int = 0
+
+
+@dataclass
+class SdpaCapture:
+    """Inputs and output of selected calls of the SDPA replacement, by 0-based call index (one call
+    per decoder layer in a prefill): {"q", "k", "v", "out", "scale", "is_causal"}."""
+    calls: tuple[int, ...]
+    records: dict[int, dict[str, object]] = field(default_factory=dict)
 
 
 def build_model(*, seed: int = 0, layers: int | None = None, dtype: torch.dtype = torch.bfloat16,
@@ -78,9 +89,10 @@ def _unsupported(reason: str):
 
 @contextlib.contextmanager
 def patched_sdpa_with_gfx950(*, allow_causal: bool = True, stats: BackendUseStats | None = None,
-                             variant: str = "sliced") -> Iterator[None]:
+                             variant: str = "sliced", capture: SdpaCapture | None = None) -> Iterator[None]:
     """Replace F.scaled_dot_product_attention with the gfx950 kernel for the duration."""
     original = F.scaled_dot_product_attention
+    call_index = 0
 
     def replacement(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
                     enable_gqa=False):
@@ -94,9 +106,14 @@ def patched_sdpa_with_gfx950(*, allow_causal: bool = True, stats: BackendUseStat
             _unsupported(f"tensors on {query.device}")
         if query.shape[1] != key.shape[1] and not enable_gqa:
             _unsupported("head counts differ but enable_gqa=False")
+        nonlocal call_index
         if stats is not None:
             stats.calls += 1
-        return flash_atten.sdpa(query, key, value, is_causal=is_causal, scale=scale, variant=variant)
+        out = flash_atten.sdpa(query, key, value, is_causal=is_causal, scale=scale, variant=variant)
+        if capture is not None and call_index in capture.calls:
+            capture.records[call_index] = dict(q=query, k=key, v=value, out=out, scale=scale, is_causal=is_causal)
+        call_index += 1
+        return out
 
     F.scaled_dot_product_attention = replacement
     try:
@@ -126,31 +143,36 @@ def time_ttft_ms(model, input_ids: torch.Tensor, *, warmup: int = 2, iters: int 
     return {"mean_ms": statistics.mean(times), "p50_ms": statistics.median(times), "min_ms": min(times)}
 
 
-def verify_against_torch(model, input_ids: torch.Tensor, *, variant: str = "sliced") -> dict[str, object]:
-    """Final-token logits with the gfx950 kernel vs torch's own SDPA (rtol=atol=0.1, argmax).
+def verify_against_torch(model, input_ids: torch.Tensor, *, variant: str = "sliced",
+                         capture: SdpaCapture | None = None) -> dict[str, object]:
+    """Final-token logits with the gfx950 kernel vs torch's own SDPA: allclose(rtol=atol=0.1) and
+    argmax, the reference's criterion (ttft.py:415-446); `passed` is their conjunction.
 
-    Also reports the noise floor: the same comparison between torch's default SDPA backend and its
-    math backend. Low-precision activations through many layers make two correct attention
-    implementations disagree by that much; `within_noise_floor` asks that ours stays within twice
-    the torch-vs-torch difference (or the 0.1 tolerance, whichever is larger)."""
+    Also reported: the same comparison between torch's default SDPA backend and its math backend
+    (`torch_default_vs_math_*`). bf16 activations through many layers make two correct attention
+    implementations disagree by about that much, so a failed allclose next to a torch-vs-torch
+    deviation of the same size says the tolerance, not the kernel, is at its limit."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     reference = prefill_logits(model, input_ids).float()
     with sdpa_kernel(SDPBackend.MATH):
         reference_math = prefill_logits(model, input_ids).float()
     stats = BackendUseStats()
-    with patched_sdpa_with_gfx950(stats=stats, variant=variant):
+    with patched_sdpa_with_gfx950(stats=stats, variant=variant, capture=capture):
         ours = prefill_logits(model, input_ids).float()
     diff = (ours - reference).abs()
-    floor = float((reference_math - reference).abs().max())
+    allclose = bool(torch.allclose(ours, reference, rtol=0.1, atol=0.1))
+    argmax = bool(torch.equal(ours.argmax(-1), reference.argmax(-1)))
     return {
-        "allclose_rtol_atol_0p1": bool(torch.allclose(ours, reference, rtol=0.1, atol=0.1)),
-        "argmax_match": bool(torch.equal(ours.argmax(-1), reference.argmax(-1))),
+        "passed": allclose and argmax,
+        "allclose_rtol_atol_0p1": allclose,
+        "argmax_match": argmax,
         "max_abs_diff": float(diff.max()),
         "mean_abs_diff": float(diff.mean()),
         "max_abs_diff_vs_math_backend": float((ours - reference_math).abs().max()),
-        "noise_floor_torch_default_vs_math": floor,
-        "within_noise_floor": float(diff.max()) <= max(2.0 * floor, 0.1),
+        "torch_default_vs_math_allclose_rtol_atol_0p1": bool(
+            torch.allclose(reference_math, reference, rtol=0.1, atol=0.1)),
+        "torch_default_vs_math_max_abs_diff": float((reference_math - reference).abs().max()),
         "logit_abs_max": float(reference.abs().max()),
         "kernel_calls": stats.calls,
     }
@@ -176,10 +198,12 @@ def run(prompt_lens: list[int], *, layers: int | None = None, seed: int = 0, var
             "speedup": torch_time["p50_ms"] / ours_time["p50_ms"],
             "verification": check,
         }
-        print(f"[ttft] S={prompt_len}: gfx950 {ours_time['p50_ms']:.2f} ms, torch SDPA {torch_time['p50_ms']:.2f} ms, "
-              f"max|dlogit|={check['max_abs_diff']:.3e} (torch default vs math: "
-              f"{check['noise_floor_torch_default_vs_math']:.3e}; |logit| <= {check['logit_abs_max']:.2f}), "
-              f"argmax_match={check['argmax_match']}", flush=True)
+        print(f"[ttft] S={prompt_len}: gfx950 {ours_time['p50_ms']:.2f} ms, torch SDPA {torch_time['p50_ms']:.2f} ms; "
+              f"vs torch: allclose(0.1)={check['allclose_rtol_atol_0p1']} max|dlogit|={check['max_abs_diff']:.3e} "
+              f"argmax_match={check['argmax_match']}; torch default vs math: "
+              f"allclose(0.1)={check['torch_default_vs_math_allclose_rtol_atol_0p1']} "
+              f"max|dlogit|={check['torch_default_vs_math_max_abs_diff']:.3e}; |logit| <= "
+              f"{check['logit_abs_max']:.2f}", flush=True)
         results.append(row)
     return results
 
@@ -202,7 +226,11 @@ def main(argv: list[str] | None = None) -> int:
     if args.json:
         with open(args.json, "w") as fh:
             json.dump(results, fh, indent=1)
-    ok = all(r["verification"]["argmax_match"] and r["verification"]["within_noise_floor"] for r in results)
+    # the reference's pass rule (ttft.py:441-442): allclose(rtol=atol=0.1) and argmax, every prompt
+    ok = all(r["verification"]["passed"] for r in results)
+    if not ok:
+        print("[ttft] FAILED the reference criterion allclose(rtol=atol=0.1) + argmax for prompt lengths "
+              f"{[r['prompt_len'] for r in results if not r['verification']['passed']]}", flush=True)
     return 0 if ok else 2
 
 

@@ -70,12 +70,6 @@ def _next_power_of_two(x: int) -> int:
     return 1 << (x - 1).bit_length()
 
 
-def next_power_of_two(x: int) -> int:
-    if x <= 0:
-        raise ValueError("x must be positive")
-    return 1 << (x - 1).bit_length()
-
-
 def _get_max_shared_mem_bytes() -> int:
     return int(get_sm_resource_limits()["available_shared_memory_bytes_per_sm"])
 
@@ -231,18 +225,6 @@ class FlashAttentionTuner(Tuner):
 
     def _allow_block_dmodel_smaller_than_d(self) -> bool:
         return False
-
-    def _power_of_two_candidates(self, upper_bound: int, minimum: int = 1) -> list[int]:
-        values: list[int] = []
-        value = 1 << (max(minimum, upper_bound) - 1).bit_length()
-        while value >= minimum:
-            values.append(min(value, upper_bound))
-            value //= 2
-        deduped: list[int] = []
-        for value in values:
-            if value not in deduped and value >= minimum:
-                deduped.append(value)
-        return deduped
 
     # -- resources ------------------------------------------------------------------------------
 
@@ -508,10 +490,6 @@ class FlashAttentionBlockDNomaskTuner(FlashAttentionTuner):
     already fills the GPU). Keeps the reference's 9-argument layout (tuner.py:640-650)."""
 
     KERNEL_NAME = "_flash_attn_fwd_kernel_block_d_nomask_contiguous"
-
-    def __init__(self, *args, **kwargs):
-        super().__init__(*args, **kwargs)
-        self.max_tile_length = 128
 
     def _allow_block_dmodel_smaller_than_d(self) -> bool:
         return True

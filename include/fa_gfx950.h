@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 enum {
   FA_OK = 0,
@@ -44,8 +44,17 @@ enum { FA_DTYPE_F16 = 0, FA_DTYPE_BF16 = 1 };
 enum { FA_VARIANT_BASIC = 0, FA_VARIANT_OPT = 1, FA_VARIANT_SLICED = 2 };
 
 /* One attention tile configuration. block_m = waves * rows_per_wave (rows_per_wave in {32, 64});
- * block_n = KV rows per LDS tile; stages = K/V LDS buffers (1 single-buffered, 2 double-buffered);
- * splits = KV splits of the sliced variant (1 = no split, no merge pass). */
+ * block_n = KV rows per LDS tile; splits = KV splits of the sliced variant (1 = no split, no merge
+ * pass). stages selects the K/V pipeline of the optimized and sliced variants (basic always runs
+ * stages 1):
+ *   1  one K/V LDS buffer, staged through registers;
+ *   2  double-buffered K/V LDS tiles, staged through registers;
+ *   3  software-pipelined kernel: K/V reach a ring of LDS tiles by LDS-DMA, and the QK^T MFMAs of
+ *      tile u+1 run beside the softmax of tile u. Its addressing needs
+ *      (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32 bytes and row strides >= D; when
+ *      a launch breaks either rule, fa_fwd runs the stages=2 kernel of the same block_m and waves
+ *      instead (same block_n where built, else 64). fa_fwd_supported() reports a stages=3 tile
+ *      as built only when that fallback is built too. */
 typedef struct {
   int32_t block_m;
   int32_t block_n;
@@ -92,15 +101,19 @@ typedef struct {
   int32_t group_m;
 } gemm_tile;
 
-/* Per-kernel resources, read from this library's own gfx950 code object. */
+/* Per-kernel resources. vgprs, agprs, sgprs, scratch_bytes and occupancy come from a table that
+ * the build generates from the compiler's resource-usage report for each gfx950 kernel and links
+ * into the library; lds_bytes and max_threads are read from the loaded kernel at run time
+ * (hipFuncGetAttributes). */
 typedef struct {
-  int32_t vgprs;          /* architectural VGPRs per lane                  */
-  int32_t agprs;          /* accumulation VGPRs per lane (-1 if unknown)   */
-  int32_t sgprs;          /* scalar registers per wave (-1 if unknown)     */
-  int32_t lds_bytes;      /* static LDS per workgroup                      */
-  int32_t scratch_bytes;  /* private (spill) bytes per lane                */
-  int32_t threads;        /* threads per workgroup                         */
-  int32_t max_threads;    /* largest workgroup the kernel accepts          */
+  int32_t vgprs;          /* architectural VGPRs per lane                          */
+  int32_t agprs;          /* accumulation VGPRs per lane                           */
+  int32_t sgprs;          /* scalar registers per wave                             */
+  int32_t lds_bytes;      /* static LDS per workgroup                              */
+  int32_t scratch_bytes;  /* private (spill) bytes per lane                        */
+  int32_t threads;        /* threads per workgroup                                 */
+  int32_t max_threads;    /* largest workgroup the kernel accepts                  */
+  int32_t occupancy;      /* waves per SIMD the register and LDS budgets allow     */
 } fa_resources;
 
 /* Device limits (the keys of exceptions.py:766-774, in gfx950 terms). */
@@ -148,8 +161,9 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
 
 int gemm_f16_supported(const gemm_tile* tile);
 
-/* Resources of one built kernel: op 0 = attention (variant, dtype, D, tile), op 1 = GEMM
- * (gtile). Needs a device (hipFuncGetAttributes). */
+/* Resources of one built kernel: op 0 = attention (variant, dtype, D, tile; the kernel that tile
+ * resolves to, before any stages=3 fallback), op 1 = GEMM (gtile; the default deep-ring kernel).
+ * Needs a device (hipFuncGetAttributes). */
 int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
                         const gemm_tile* gtile, fa_resources* out);
 

@@ -182,3 +182,90 @@ def test_gemm_parity(gpu):
         c = cd.float().cpu().numpy()
         rel = float(np.linalg.norm(c - ref) / np.linalg.norm(ref))
         assert rel <= 1e-3, rel
+
+
+def _strided_kv(x: np.ndarray, row_stride: int, dtype, device) -> torch.Tensor:
+    """[1, 1, N, D] device view whose rows sit row_stride elements apart (row_stride < D overlaps
+    neighbouring rows; those rows then hold what the later row wrote, mirrored in the returned
+    host copy)."""
+    _, _, N, D = x.shape
+    base = torch.zeros((N - 1) * row_stride + D, dtype=dtype, device=device)
+    view = base.as_strided((1, 1, N, D), (N * row_stride, N * row_stride, row_stride, 1))
+    for n in range(N):  # row by row, so overlapping rows end up as the last writer left them
+        view[0, 0, n].copy_(torch.from_numpy(np.ascontiguousarray(x[0, 0, n])).to(dtype))
+    return view
+
+
+@pytest.mark.parametrize("why", ["short_row_stride", "span_over_4gib"])
+@pytest.mark.parametrize("D,tile_name,dtype", [(128, "pipe128", F16), (256, "pipe128n32", BF16)])
+@pytest.mark.parametrize("splits", [1, 2])
+def test_fa_pipelined_fallback(gpu, why, D, tile_name, dtype, splits):
+    """A pipelined (stages=3) tile whose addressing rules a launch breaks runs the double-buffered
+    kernel instead: K/V row stride below D (overlapping rows), and a (batch, kv-head) span of
+    (N + block_n) * row stride * 2 bytes beyond 2^32. Both against the oracle on the same data."""
+    N, M = (40, 64) if why == "span_over_4gib" else (300, 96)
+    row_stride = 48 * 1024 * 1024 if why == "span_over_4gib" else D // 2
+    print(f"[fa_abi] pipelined fallback {why} D={D} {dtype} splits={splits} N={N} stride={row_stride}", flush=True)
+    var, bm, bn, waves, stages = TILES[tile_name]
+    assert (N + bn) * row_stride * 2 > 2 ** 32 or row_stride < D
+    q, k, v = make_qkv(4242 + D, 1, 1, 1, M, N, D, dtype)
+    dev = "cuda:0"
+    kd, vd = _strided_kv(k, row_stride, dtype, dev), _strided_kv(v, row_stride, dtype, dev)
+    # what the kernel reads: the device rows as they ended up (overlaps resolved by the last row)
+    k_seen, v_seen = (t.float().cpu().numpy() for t in (kd, vd))
+    qd = to_device(q, dtype, dev)
+    o = torch.empty_like(qd)
+    lse = torch.empty((1, 1, M), dtype=torch.float32, device=dev)
+    ws = None
+    nbytes = hip_lib.workspace_bytes(1, 1, M, D, splits)
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    hip_lib.fa_fwd(qd, kd, vd, o, lse, sm_scale=D ** -0.5, causal=False, variant=SLICED if splits > 1 else OPT,
+                   tile=hip_lib.make_tile(bm, bn, waves, stages, splits), workspace=ws)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.attention(q, k_seen, v_seen, causal=False)
+    assert max_abs(o.float().cpu().numpy(), o_ref) <= ATOL[dtype]
+    assert max_abs(lse.cpu().numpy(), lse_ref) <= 1e-3
+    del kd, vd
+    torch.cuda.empty_cache()
+
+
+def test_kernel_resources_live_match_compiled_table(gpu):
+    """fa_kernel_resources for every built attention tile and GEMM tile: registers, scratch and
+    occupancy from the table linked into the library, LDS and the workgroup limit from the loaded
+    kernel; both must agree with kernel_resources.json (the same compiler remarks)."""
+    import gfx950_configs
+
+    table = hip_lib.compiled_resources()
+    checked = 0
+    for variant in (BASIC, OPT, SLICED):
+        for dtype in (F16, BF16):
+            for D in (64, 128, 256):
+                for bm, bn, waves, stages in gfx950_configs.FA_TILE_SPACE:
+                    for splits in ((1, 4) if variant == SLICED else (1,)):
+                        t = hip_lib.make_tile(bm, bn, waves, stages, splits)
+                        if not hip_lib.fa_fwd_supported(variant, dtype, D, t):
+                            continue
+                        live = hip_lib.kernel_resources_live(0, variant=variant, dtype=dtype, D=D, tile=t)
+                        raw = table[hip_lib.fwd_kernel_symbol(variant, dtype, D, t)]
+                        _compare_resources(live, raw, waves)
+                        checked += 1
+    for bm, bn, bk, waves in gfx950_configs.GEMM_TILE_SPACE:
+        g = hip_lib.GemmTile(bm, bn, bk, waves, 8)
+        if not hip_lib.gemm_supported(g):
+            continue
+        live = hip_lib.kernel_resources_live(1, gtile=g)
+        _compare_resources(live, table[hip_lib.gemm_kernel_symbol(g)], waves)
+        checked += 1
+    print(f"[fa_abi] kernel resources checked for {checked} launches", flush=True)
+    assert checked >= 40
+
+
+def _compare_resources(live: dict, raw: dict, waves: int) -> None:
+    assert live["vgprs"] == raw["VGPRs"]
+    assert live["agprs"] == raw["AGPRs"]
+    assert live["sgprs"] == raw["TotalSGPRs"]
+    assert live["scratch_bytes"] == raw["ScratchSize [bytes/lane]"]
+    assert live["occupancy"] == raw["Occupancy [waves/SIMD]"]
+    assert live["lds_bytes"] == raw["LDS Size [bytes/block]"]
+    assert live["threads"] == waves * 64 <= live["max_threads"]

@@ -55,16 +55,20 @@ def test_gemm_tails_all_tiles(gpu, shape):
         assert bool((cbuf[:, N:] == sentinel).all()), tile
 
 
-def test_gemm_tails_convenience_entry(gpu):
-    """mma.matmul takes tail shapes (the reference selector still raises for them)."""
-    M, N, K = 777, 1032, 264  # contiguous B: 16-byte rows need N % 8 == 0
-    print("[gemm_tails] mma.matmul", flush=True)
+@pytest.mark.parametrize("shape", [(777, 1032, 264), (300, 100, 64), (65, 1028, 520)],
+                         ids=["n_mod8_0", "n_mod8_4", "n_mod8_4_deep"])
+def test_gemm_tails_convenience_entry(gpu, shape):
+    """mma.matmul takes tail shapes (the reference selector still raises for them), N % 8 == 4
+    included (B is restaged into rows of a multiple of 8 elements)."""
+    M, N, K = shape
+    print(f"[gemm_tails] mma.matmul {M}x{N}x{K}", flush=True)
     with pytest.raises(ValueError):
         mma._select_2d_contiguous_config(M, N, K)
     a = oracle.round_to(oracle.portable_uniform(31, (M, K), -1, 1), 0)
     b = oracle.round_to(oracle.portable_uniform(32, (K, N), -1, 1), 0)
     c = mma.matmul(to_device(a, torch.float16, "cuda:0"), to_device(b, torch.float16, "cuda:0"))
     torch.cuda.synchronize()
+    assert c.is_contiguous() and tuple(c.shape) == (M, N)
     ref = oracle.gemm(a, b)
     assert float(np.linalg.norm(c.float().cpu().numpy() - ref) / np.linalg.norm(ref)) <= 1e-3
     assert cfgs.choose_gemm_tile_any(M, N, K)[:3] != ()

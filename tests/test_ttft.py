@@ -78,3 +78,53 @@ def test_small_qwen2_prefill_matches_torch_sdpa(gpu):
     assert check["allclose_rtol_atol_0p1"], check
     assert check["argmax_match"], check
     assert np.isfinite(check["max_abs_diff"])
+
+
+def _layer_rows_vs_oracle(rec: dict, *, heads=(0, 5, 11), rows_per_head: int = 16, seed: int = 0) -> float:
+    """Max |O - O_oracle| over sampled rows of a captured attention call (first and last row of
+    each listed head included). q is [1, H, S, D] (a strided view of the projection), k/v carry
+    the kv heads; query head h reads kv head h // (H // H_kv)."""
+    q, k, v, out = (rec[n] for n in ("q", "k", "v", "out"))
+    _, H, S, D = q.shape
+    group = H // k.shape[1]
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for h in heads:
+        rows = np.sort(rng.choice(S, size=rows_per_head, replace=False))
+        rows[0], rows[-1] = 0, S - 1
+        qs = q[0, h].float().cpu().numpy()[None, None]
+        ks = k[0, h // group].float().cpu().numpy()[None, None]
+        vs = v[0, h // group].float().cpu().numpy()[None, None]
+        o_ref, _ = oracle.attention_rows(qs, ks, vs, rows, causal=bool(rec["is_causal"]), scale=rec["scale"])
+        got = out[0, h].float().cpu().numpy()[rows]
+        worst = max(worst, max_abs(got, o_ref))
+    return worst
+
+
+@pytest.mark.gpu
+def test_qwen25_1p5b_full_prefill_layers_vs_oracle(gpu):
+    """BASELINE configs[4] at full size: the 28-layer, vocab-151936 Qwen2.5-1.5B architecture (random
+    init, bf16), causal prefill of 4096 and 16384 seeded tokens with every attention call on the
+    gfx950 kernel. Asserted: the attention output of the first, a middle and the last layer against
+    the oracle on sampled rows of three heads (bf16 bound 3e-2), one kernel call per layer, and the
+    final-token argmax against torch's own SDPA. Recorded (printed as one JSON line per prompt):
+    the reference's allclose(rtol=atol=0.1) on the final logits (ttft.py:415-446) and the same
+    comparison between torch's default and math SDPA backends."""
+    import json
+
+    print("[ttft] building the 28-layer Qwen2.5-1.5B-architecture model", flush=True)
+    model = ttft_qwen.build_model(seed=0)
+    assert model.config.num_hidden_layers == 28 and model.config.vocab_size == 151936
+    layers = model.config.num_hidden_layers
+    for S in (4096, 16384):
+        print(f"[ttft] full prefill S={S}", flush=True)
+        ids = ttft_qwen.make_prompt(S, model.config.vocab_size, seed=S)
+        cap = ttft_qwen.SdpaCapture(calls=(0, layers // 2, layers - 1))
+        check = ttft_qwen.verify_against_torch(model, ids, capture=cap)
+        layer_err = {i: _layer_rows_vs_oracle(cap.records[i], seed=S + i) for i in cap.calls}
+        print("[ttft] " + json.dumps({"prompt_len": S, "layer_max_abs_vs_oracle": layer_err, **check}), flush=True)
+        del cap
+        torch.cuda.empty_cache()
+        assert check["kernel_calls"] == layers
+        assert all(err <= 3e-2 for err in layer_err.values()), layer_err
+        assert check["argmax_match"], check

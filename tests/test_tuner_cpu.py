@@ -79,13 +79,6 @@ def test_gqa_shapes_accepted_and_sliced_allows_small_block_dmodel():
                                     tune_args=FlashAttenTuneArguments(BLOCK_DMODEL=32))
 
 
-def test_power_of_two_candidates_restatement():
-    t = FlashAttentionTuner(Q, Q, Q, 2, causal=False, return_lse=False)
-    assert t._power_of_two_candidates(256, minimum=16) == [256, 128, 64, 32, 16]
-    assert t._power_of_two_candidates(100, minimum=16) == [100, 64, 32, 16]
-    assert t._power_of_two_candidates(8, minimum=16) == []  # min(16, 8) = 8 is filtered by the minimum
-
-
 # ---- launch layouts (tuner.py:264-305, 639-658) ------------------------------------------------------
 
 
