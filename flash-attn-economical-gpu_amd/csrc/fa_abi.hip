@@ -6,10 +6,19 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "fa_kernels.h"
 #include "../../include/fa_gfx950.h"
+
+// Split-KV partials of fa_fwd_noalloc (no allocation on that path). Each GPU holds its own copy
+// of this array for the life of the process; its address on a device comes from
+// hipGetSymbolAddress with that device current, once, and only that address is handed to kernels
+// (the array's name in host code is a host-side stand-in, not a device address). Nothing in it
+// needs to start at zero: every split writes all of its partial rows before the merge reads them.
+constexpr int64_t kScratchBytes = FA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
@@ -123,6 +132,27 @@ const fa::FaKernelEntry* double_buffered_fallback(const fa::FaKernelEntry* e) {
   return fb;
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(FA_EHIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FA_EINVAL, "device index %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(FA_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FA_OK;
+}
+
 const fa::KernelResourceRow* find_resource_row(const char* symbol) {
   for (int i = 0; i < fa::kKernelResourceRowCount; ++i)
     if (std::strcmp(fa::kKernelResourceRows[i].symbol, symbol) == 0) return &fa::kKernelResourceRows[i];
@@ -182,7 +212,7 @@ int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* t
   return ok();
 }
 
-// The body of fa_fwd: the split-KV workspace comes in as (ws, ws_bytes).
+// The body of fa_fwd and fa_fwd_noalloc: the split-KV workspace comes in as (ws, ws_bytes).
 static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
   bool split = false;
   int code = FA_OK;
@@ -293,6 +323,24 @@ static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* st
 int fa_fwd(const fa_fwd_args* a, void* stream) {
   if (a == nullptr) return fail(FA_EINVAL, "null argument block");
   return launch_fwd(a, a->workspace, a->workspace_bytes, stream);
+}
+
+int fa_fwd_noalloc(const fa_fwd_args* a, void* stream) {
+  if (a == nullptr) return fail(FA_EINVAL, "null argument block");
+  if (a->workspace != nullptr || a->workspace_bytes != 0)
+    return fail(FA_EINVAL, "fa_fwd_noalloc takes no workspace (workspace must be NULL, workspace_bytes 0)");
+  const int splits = a->tile.splits < 1 ? 1 : a->tile.splits;
+  if (a->variant != FA_VARIANT_SLICED || splits == 1) return launch_fwd(a, nullptr, 0, stream);
+  const int64_t need = fa_fwd_workspace_bytes(a->B, a->H, a->M, a->D, splits);
+  if (need > kScratchBytes)
+    return fail(FA_EWORKSPACE,
+                "fa_fwd_noalloc: split-KV partials of %lld bytes exceed its static scratch of %lld bytes "
+                "(B=%d H=%d M=%d D=%d splits=%d); use fa_fwd with a workspace, or fewer splits",
+                (long long)need, (long long)kScratchBytes, a->B, a->H, a->M, a->D, splits);
+  void* ptr = nullptr;
+  const int code = scratch_of_current_device(&ptr);
+  if (code != FA_OK) return code;
+  return launch_fwd(a, ptr, kScratchBytes, stream);
 }
 
 int gemm_f16_supported(const gemm_tile* tile) {

@@ -106,6 +106,7 @@ SIGNATURES = {
     "fa_abi_version": (ctypes.c_int, []),
     "fa_last_error": (ctypes.c_char_p, []),
     "fa_fwd": (ctypes.c_int, [ctypes.POINTER(FaFwdArgs), ctypes.c_void_p]),
+    "fa_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(FaFwdArgs), ctypes.c_void_p]),
     "fa_fwd_workspace_bytes": (
         ctypes.c_int64,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
@@ -283,6 +284,31 @@ def fa_fwd(
     args = _fwd_args(q, k, v, o, lse, sm_scale=sm_scale, causal=causal, variant=variant, tile=tile,
                      workspace=workspace)
     check(lib.fa_fwd(ctypes.byref(args), _stream_ptr(q.device)), "fa_fwd")
+
+
+# Size of the static device array fa_fwd_noalloc keeps its split-KV partials in
+# (FA_NOALLOC_SCRATCH_BYTES in include/fa_gfx950.h).
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def fa_fwd_noalloc(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor | None,
+    *,
+    sm_scale: float,
+    causal: bool,
+    variant: int,
+    tile: FaTile,
+) -> None:
+    """fa_fwd with the split-KV partials in the library's static per-GPU scratch array (no device
+    allocation by the library or here). Calls on one GPU share that array: overlapping calls race.
+    Raises ValueError when the partials need more than NOALLOC_SCRATCH_BYTES."""
+    lib = load()
+    args = _fwd_args(q, k, v, o, lse, sm_scale=sm_scale, causal=causal, variant=variant, tile=tile, workspace=None)
+    check(lib.fa_fwd_noalloc(ctypes.byref(args), _stream_ptr(q.device)), "fa_fwd_noalloc")
 
 
 def gemm_f16(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, tile: GemmTile) -> None:

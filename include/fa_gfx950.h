@@ -18,6 +18,7 @@
  *   gemm_f16                           <- _matmul_contiguous_kernel[grid](a,b,c,M,N,K,...)  mma.py:8-21
  *   fa_device_limits                   <- get_sm_resource_limits()                         exceptions.py:760-775
  *   fa_kernel_resources                <- Triton compile metadata (shared, n_regs)          tuner.py:341-376
+ *   fa_fwd_noalloc                     (no counterpart: fa_fwd for callers that cannot allocate)
  */
 #ifndef FA_GFX950_H
 #define FA_GFX950_H
@@ -135,6 +136,17 @@ const char* fa_last_error(void);
 
 /* Attention forward; launches on `stream`. */
 int fa_fwd(const fa_fwd_args* args, void* stream);
+
+/* fa_fwd without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The split-KV partials go to a
+ * static device array of FA_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends;
+ * args->workspace must be NULL and args->workspace_bytes 0. A launch whose partials
+ * (fa_fwd_workspace_bytes) exceed the array fails with FA_EWORKSPACE before anything runs.
+ * Calls on one GPU share its array: calls that overlap (other streams, other threads) race, so
+ * the caller orders them. Launches without splits use no scratch and behave as fa_fwd. No
+ * counterpart in the reference. */
+#define FA_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int fa_fwd_noalloc(const fa_fwd_args* args, void* stream);
 
 /* Bytes of split-KV workspace fa_fwd needs for these sizes (0 when splits <= 1). */
 int64_t fa_fwd_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t D, int32_t splits);
