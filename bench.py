@@ -8,9 +8,12 @@ test_mma.py:78-83) is reported in the `gemm` object. Each launch is timed with H
 on the stream the kernels are launched on (torch's current stream), and the mean launch duration
 feeds `roofline.achieved`. The CPU baseline is the reference's own CPU path (torch SDPA math
 backend on fp32 CPU copies, test_flash_atten.py:459-461, 498-499; CPU torch.matmul, test_mma.py:
-260-261) on a bounded sample, extrapolated to the full workload.
+260-261), measured on the box's host cores: attention on one (b, h) slice of the headline and on
+config 1, the GEMM in fp32 at 8192^3 and in fp16 at the reference's published 8192x8192x256.
+Beside each kernel, AMD's own implementation on the same GPU (torch.matmul -> hipBLASLt; torch's
+scaled_dot_product_attention) is timed in alternating rounds with ours (`vendor`).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--variant optimized]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-vendor] [--variant optimized]
 """
 from __future__ import annotations
 
@@ -69,56 +72,109 @@ def _time_launches(torch, fn, steps: int, warmup: int):
     return outer_s.elapsed_time(outer_e), per
 
 
-def _cpu_baseline_attention(torch, B, H, N, D, slices: int, sample_n: int):
-    """torch CPU SDPA (math backend) on `slices` query blocks of `sample_n` rows of one (b, h) slice
-    against all N keys; the per-score time is extrapolated to B*H*N*N scores."""
+def _cpu_threads(torch) -> dict:
+    return {"cores": torch.get_num_threads(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
+
+
+def _time_cpu(fn, warmup: int, runs: int, label: str) -> list[float]:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for i in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        _log(f"cpu {label} run {i + 1}/{runs}: {times[-1] * 1e3:.1f} ms")
+    return times
+
+
+def _cpu_baseline_attention(torch, B, H, N, D):
+    """The reference's CPU path for attention (its oracle, test_flash_atten.py:459-461, 498-499):
+    torch SDPA, math backend, on fp32 copies of fp16 N(0,1) inputs.
+      * headline: one (b, h) slice [1,1,N,D] of the workload, measured; the whole workload is that
+        time x B*H (stated as extrapolated, never as measured);
+      * config 1 [1,4,512,64], 3 warm-ups + 10 timed runs, mean and p50 (test_flash_atten.py:549-571)."""
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     g = torch.Generator().manual_seed(SEED)
-    q = torch.randn(1, 1, sample_n, D, generator=g, dtype=torch.float16).float()
-    k, v = (torch.randn(1, 1, N, D, generator=g, dtype=torch.float16).float() for _ in range(2))
+
+    def inputs(shape):
+        return tuple(torch.randn(shape, generator=g, dtype=torch.float16).float() for _ in range(3))
+
     with sdpa_kernel(SDPBackend.MATH):
-        F.scaled_dot_product_attention(q, k, v)  # warm-up
-        times = []
-        for i in range(slices):
-            t0 = time.perf_counter()
-            F.scaled_dot_product_attention(q, k, v)
-            times.append(time.perf_counter() - t0)
-            _log(f"cpu sdpa block {i + 1}/{slices}: {times[-1] * 1e3:.1f} ms")
-    per_block = statistics.mean(times)
-    full_s = per_block * (N / sample_n) * B * H
-    flops = 4.0 * B * H * N * N * D
+        q, k, v = inputs((1, 1, N, D))
+        t_slice = _time_cpu(lambda: F.scaled_dot_product_attention(q, k, v), 1, 3, f"sdpa [1,1,{N},{D}]")
+        q1, k1, v1 = inputs((1, 4, 512, 64))
+        t_cfg1 = _time_cpu(lambda: F.scaled_dot_product_attention(q1, k1, v1), 3, 10, "sdpa config1 [1,4,512,64]")
+    slice_s = statistics.mean(t_slice)
+    slice_flops = 4.0 * N * N * D
+    cfg1_flops = 4.0 * 1 * 4 * 512 * 512 * 64
+    cfg1_mean, cfg1_p50 = statistics.mean(t_cfg1), statistics.median(t_cfg1)
     return {
-        "value": flops / full_s / 1e12,
+        "value": slice_flops / slice_s / 1e12,
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        **_cpu_threads(torch),
         "kind": "reference",
-        "sample": (f"torch CPU SDPA math backend on fp32 copies of fp16 inputs (the reference's oracle path); "
-                   f"{slices} timed runs of a [1,1,{sample_n},{D}] query block against {N} keys after 1 warm-up, "
-                   f"mean {per_block * 1e3:.1f} ms, extrapolated x{(N // sample_n) * B * H} to B={B} H={H} "
-                   f"N={N} ({full_s:.1f} s); affinity cores={len(os.sched_getaffinity(0))}"),
+        "sample": (f"torch CPU SDPA math backend on fp32 copies of fp16 inputs (the reference's oracle path), one "
+                   f"(b,h) slice [1,1,{N},{D}] of the headline: 1 warm-up + 3 runs, mean {slice_s * 1e3:.1f} ms "
+                   f"(measured); the whole B={B} H={H} workload would take {slice_s * B * H:.1f} s "
+                   f"(extrapolated x{B * H})"),
+        "config1": {"shape": [1, 4, 512, 64], "warmup": 3, "runs": 10, "mean_ms": round(cfg1_mean * 1e3, 3),
+                    "p50_ms": round(cfg1_p50 * 1e3, 3), "tflops_mean": cfg1_flops / cfg1_mean / 1e12,
+                    "note": "measured; BASELINE configs[0], test_flash_atten.py:549-571 protocol"},
     }
 
 
-def _cpu_baseline_gemm(torch, M, N, K, sample: tuple[int, int, int]):
-    """CPU torch.matmul fp16 (the reference's CPU path) on a bounded sample shape, rate applied by FLOP."""
-    sm, sk, sn = sample
+def _cpu_baseline_gemm(torch, M, N, K, fp16_runs: int = 1):
+    """The reference's CPU GEMM path (CPU torch.matmul, test_mma.py:260-261): fp32 at M x K x N (the
+    headline shape; 1 warm-up + 2 runs, measured) and fp16 on a 2048-row block of the reference's
+    published 8192x8192x256 (test_mma.py:42-45; `fp16_runs` runs, no warm-up). CPU fp16 GEMM runs at
+    ~1 GFLOP/s, so the whole published shape would take ~50 s; output rows are independent, so the
+    whole shape's time is the block's x 4, stated as such."""
     g = torch.Generator().manual_seed(SEED)
-    a = (torch.rand(sm, sk, generator=g) * 2 - 1).half()
-    b = (torch.rand(sk, sn, generator=g) * 2 - 1).half()
-    t0 = time.perf_counter()
-    torch.matmul(a, b)
-    dt = time.perf_counter() - t0
-    _log(f"cpu matmul {sm}x{sk}x{sn}: {dt * 1e3:.1f} ms")
+    a32 = torch.rand(M, K, generator=g) * 2 - 1
+    b32 = torch.rand(K, N, generator=g) * 2 - 1
+    t32 = _time_cpu(lambda: torch.matmul(a32, b32), 1, 2, f"matmul fp32 {M}x{K}x{N}")
+    del a32, b32
+    pm, pk, pn = 2048, 256, 8192
+    a16 = (torch.rand(pm, pk, generator=g) * 2 - 1).half()
+    b16 = (torch.rand(pk, pn, generator=g) * 2 - 1).half()
+    t16 = _time_cpu(lambda: torch.matmul(a16, b16), 0, fp16_runs, f"matmul fp16 {pm}x{pk}x{pn}")
+    s32, s16 = statistics.mean(t32), statistics.mean(t16)
     return {
-        "value": 2.0 * sm * sn * sk / dt / 1e12,
+        "value": 2.0 * M * N * K / s32 / 1e12,
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        **_cpu_threads(torch),
         "kind": "reference",
-        "sample": (f"CPU torch.matmul fp16 {sm}x{sk} @ {sk}x{sn} (test_mma.py's K=256), 1 run ({dt:.3f} s); "
-                   f"rate applied to {M}x{K}x{N}"),
+        "sample": (f"CPU torch.matmul fp32 {M}x{K} @ {K}x{N} (the headline shape in fp32; fp16 CPU GEMM at that "
+                   f"shape would run for ~15 min): 1 warm-up + 2 runs, mean {s32:.3f} s, measured"),
+        "fp16_8192x8192x256": {"block_rows_measured": pm, "block_mean_s": round(s16, 3), "runs": fp16_runs,
+                               "tflops": 2.0 * pm * pn * pk / s16 / 1e12,
+                               "whole_shape_s_extrapolated": round(s16 * 8192 / pm, 1),
+                               "note": "the reference's CPU path at its published shape (test_mma.py:42-45, "
+                                       "260-261): a 2048x256 @ 256x8192 row block measured, the whole "
+                                       "8192-row shape = 4 such blocks"},
     }
+
+
+def _alternating(torch, fns: dict, rounds: int, per_round: int) -> dict:
+    """Median launch time (ms) of each callable, timed in alternating rounds on the current stream so
+    clock and thermal drift hit every entry alike."""
+    times = {name: [] for name in fns}
+    for _ in range(rounds):
+        for name, fn in fns.items():
+            fn()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(per_round):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            times[name].append(s.elapsed_time(e) / per_round)
+    return {name: statistics.median(v) for name, v in times.items()}
 
 
 def _traffic_probe(torch, flash_atten, tuner, mma, dev) -> int:
@@ -203,6 +259,181 @@ def _traffic_summarize(fetch_csv: str, write_csv: str, out_path: Path = TRAFFIC_
     return 0
 
 
+# Counter passes for `--counters-summarize` (each within one pass's hardware limits: at most 8 SQ,
+# 4 TCC and 2 GRBM counters). Each pass profiles one `bench.py --counter-run` process.
+COUNTER_PASSES = {
+    "p1": "GRBM_GUI_ACTIVE SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
+          "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_WAVE_CYCLES",
+    "p2": "GRBM_GUI_ACTIVE SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_WAIT_INST_LDS SQ_WAIT_INST_ANY SQ_INSTS_SALU "
+          "SQ_ACTIVE_INST_MISC SQ_INSTS_SMEM SQ_WAVES",
+    "p3": "GRBM_GUI_ACTIVE SQ_WAIT_ANY SQ_ACTIVE_INST_ANY SQ_VALU_MFMA_COEXEC_CYCLES SQ_INSTS_VALU_TRANS_F32 "
+          "SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL SQ_BUSY_CU_CYCLES SQ_INSTS_BRANCH",
+    "fetch": "FETCH_SIZE",
+    "write": "WRITE_SIZE",
+}
+# Calibration launches of `--counter-run`: out = in + 1 over fp32 tensors of these sizes, the first
+# add kernels of the process (each reads and writes exactly its size once).
+CALIBRATION_MIB = (64, 256, 1024)
+
+
+def counters_command(fa_config: str, out_dir: str, fa_tile: str | None = None) -> str:
+    tile = f" --fa-tile {fa_tile}" if fa_tile else ""
+    runs = [f"rocprofv3 --pmc {c} --output-format csv -d {out_dir} -o {name} -- python -u bench.py --counter-run "
+            f"--fa-config {fa_config}{tile}" for name, c in COUNTER_PASSES.items()]
+    return " && ".join(["export TMPDIR=/tmp", *runs,
+                        f"python bench.py --counters-summarize {out_dir} --fa-config {fa_config}{tile}"])
+
+
+def _calibration_launches(torch, dev) -> None:
+    for mib in CALIBRATION_MIB:
+        src = torch.ones(mib * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.add(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+    torch.cuda.empty_cache()
+
+
+def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str | None = None) -> int:
+    """Markdown summary of the counter passes over `bench.py --counter-run --fa-config <cfg>`: per
+    kernel, the mean over its last `steps` dispatches (the bench's timed launches, after its
+    warm-up), clock and MFMA utilisation, instruction mix, LDS conflicts and calibrated HBM bytes."""
+    import csv
+    import glob
+
+    passes: dict[str, list[dict]] = {}
+    for path in sorted(glob.glob(os.path.join(directory, "*_counter_collection.csv"))):
+        name = os.path.basename(path)[: -len("_counter_collection.csv")]
+        disp: dict[int, dict] = {}
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                d = disp.setdefault(int(r["Dispatch_Id"]), {"kernel": r["Kernel_Name"], "c": {},
+                                                           "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+                d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        passes[name] = [disp[k] for k in sorted(disp)]
+    missing = set(COUNTER_PASSES) - set(passes)
+    if missing:
+        raise SystemExit(f"counter passes missing in {directory}: {sorted(missing)}")
+
+    def calib(rows, counter):
+        # torch.add's kernel (the fills that create the tensors are separate dispatches)
+        cal = [r for r in rows if "_add<" in r["kernel"]][: len(CALIBRATION_MIB)]
+        if len(cal) != len(CALIBRATION_MIB):
+            raise SystemExit("calibration dispatches not found")
+        return [mib * 1024 * 1024 / (r["c"][counter] * 1024) for mib, r in zip(CALIBRATION_MIB, cal)]
+
+    f_factors, w_factors = calib(passes["fetch"], "FETCH_SIZE"), calib(passes["write"], "WRITE_SIZE")
+    f_factor, w_factor = statistics.mean(f_factors), statistics.mean(w_factors)
+
+    cfg = FA_CONFIGS[fa_config]
+    B, H, N, D = cfg["B"], cfg["H"], cfg["N"], cfg["D"]
+    fa_flops = 4.0 * B * H * D * (N * (N + 1) / 2 if cfg["causal"] else N * N)
+    M_, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
+    kernels = {
+        "attention": ("fa_fwd_kernel", fa_flops, 4 * B * H * N * D * 2),
+        "gemm": ("gemm_f16", 2.0 * M_ * Ng * K, 2 * (M_ * K + K * Ng + M_ * Ng)),
+        # hipBLASLt's kernel for the same GEMM (torch.matmul in the alternating vendor rounds; the
+        # fp32 product of the parity check is a Cijk_..._S_B_ kernel and is skipped)
+        "gemm hipBLASLt": ("Cijk_", 2.0 * M_ * Ng * K, 2 * (M_ * K + K * Ng + M_ * Ng)),
+    }
+
+    def is_kernel(name: str, needle: str) -> bool:
+        return needle in name and not (needle == "Cijk_" and "_S_B_" in name)
+
+    out = {}
+    for key, (needle, flops, algo_bytes) in kernels.items():
+        per_pass = {}
+        for name, rows in passes.items():
+            hits = [r for r in rows if is_kernel(r["kernel"], needle)][-steps:]
+            if not hits:
+                break
+            per_pass[name] = None
+        if len(per_pass) != len(passes):
+            if key.endswith("hipBLASLt"):
+                continue  # vendor rounds not in these passes
+            raise SystemExit(f"no {needle} dispatch in some pass")
+        for name, rows in passes.items():
+            hits = [r for r in rows if is_kernel(r["kernel"], needle)][-steps:]
+            per_pass[name] = {"kernel": hits[0]["kernel"], "n": len(hits),
+                              "ns": statistics.mean(r["ns"] for r in hits),
+                              "c": {c: statistics.mean(r["c"][c] for r in hits) for c in hits[0]["c"]}}
+        p1, p2, p3 = per_pass["p1"], per_pass["p2"], per_pass["p3"]
+        c1, c2, c3 = p1["c"], p2["c"], p3["c"]
+        secs = p1["ns"] * 1e-9
+        cycles = c1["GRBM_GUI_ACTIVE"] / 8  # summed over the 8 XCDs
+        rd = per_pass["fetch"]["c"]["FETCH_SIZE"] * 1024 * f_factor
+        wr = per_pass["write"]["c"]["WRITE_SIZE"] * 1024 * w_factor
+        out[key] = {
+            "kernel": p1["kernel"], "dispatches_averaged": p1["n"],
+            "duration_ms_p1": p1["ns"] * 1e-6, "duration_ms_p2": p2["ns"] * 1e-6,
+            "tflops_at_p1_duration": flops / secs / 1e12,
+            "clock_ghz": cycles / secs / 1e9,
+            "mfma_busy": c1["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * cycles),
+            "mfma_insts": c1["SQ_INSTS_MFMA"],
+            "mfma_flop_32x32x16": c1["SQ_INSTS_MFMA"] * 32768,
+            "valu_per_mfma": c1["SQ_INSTS_VALU"] / c1["SQ_INSTS_MFMA"],
+            "lds_per_mfma": c1["SQ_INSTS_LDS"] / c1["SQ_INSTS_MFMA"],
+            "lds_bank_conflict_rate": c1["SQ_LDS_BANK_CONFLICT"] / max(c1["SQ_LDS_IDX_ACTIVE"], 1.0),
+            "valu_active_per_wave_cycle": c2["SQ_ACTIVE_INST_VALU"] / c1["SQ_WAVE_CYCLES"],
+            "lds_wait_per_wave_cycle": c2["SQ_WAIT_INST_LDS"] / c1["SQ_WAVE_CYCLES"],
+            "any_wait_per_wave_cycle": c2["SQ_WAIT_INST_ANY"] / c1["SQ_WAVE_CYCLES"],
+            "salu_per_mfma": c2["SQ_INSTS_SALU"] / c1["SQ_INSTS_MFMA"],
+            "wait_any_per_wave_cycle": c3["SQ_WAIT_ANY"] / c1["SQ_WAVE_CYCLES"],
+            "issue_any_per_wave_cycle": c3["SQ_ACTIVE_INST_ANY"] / c1["SQ_WAVE_CYCLES"],
+            "valu_mfma_coexec_of_mfma_busy": c3["SQ_VALU_MFMA_COEXEC_CYCLES"] / max(c1["SQ_VALU_MFMA_BUSY_CYCLES"], 1.0),
+            "trans_per_mfma": c3["SQ_INSTS_VALU_TRANS_F32"] / c1["SQ_INSTS_MFMA"],
+            "lds_fifo_full_per_cu_cycle": (c3["SQ_LDS_DATA_FIFO_FULL"] + c3["SQ_LDS_CMD_FIFO_FULL"]) / (256 * cycles),
+            "branches_per_mfma": c3["SQ_INSTS_BRANCH"] / c1["SQ_INSTS_MFMA"],
+            "hbm_read_bytes": rd, "hbm_write_bytes": wr, "hbm_bytes": rd + wr,
+            "algorithmic_bytes": algo_bytes, "hbm_ratio_to_algorithmic": (rd + wr) / algo_bytes,
+        }
+    lines = [f"# Counters on warmed launches: attention `{fa_config}` and the 8192³ GEMM", "",
+             "Command (repository root, one MI355X):", "", "```", counters_command(fa_config, directory, fa_tile), "```", "",
+             f"Each pass is one `bench.py --counter-run` process: {len(CALIBRATION_MIB)} calibration launches "
+             f"(out = in + 1 over fp32 tensors of {', '.join(f'{m} MiB' for m in CALIBRATION_MIB)}), then the bench's "
+             f"own warm-up and timed launches of the attention forward and the GEMM. Figures are means over "
+             f"each kernel's last {steps} dispatches (the timed ones); durations are the counter passes' own "
+             f"(kernels run one at a time under counter collection).", "",
+             f"HBM calibration: FETCH_SIZE x 1024 x {f_factor:.3f} and WRITE_SIZE x 1024 x {w_factor:.3f} bytes "
+             f"(per-size factors: read {', '.join(f'{x:.3f}' for x in f_factors)}; "
+             f"write {', '.join(f'{x:.3f}' for x in w_factors)}).", "",
+             "| | " + " | ".join(out) + " |", "|---|" + "---|" * len(out)]
+    fields = [("kernel", "kernel", "{}"), ("duration (ms, pass 1 / 2)", None, None),
+              ("TFLOP/s at that duration", "tflops_at_p1_duration", "{:.0f}"), ("clock (GHz)", "clock_ghz", "{:.2f}"),
+              ("MFMA busy (of SIMD-cycles)", "mfma_busy", "{:.3f}"), ("MFMA instructions", "mfma_insts", "{:.4g}"),
+              ("VALU instructions per MFMA (MFMA included)", "valu_per_mfma", "{:.2f}"),
+              ("LDS instructions per MFMA", "lds_per_mfma", "{:.2f}"), ("SALU per MFMA", "salu_per_mfma", "{:.2f}"),
+              ("LDS bank-conflict cycles / LDS active", "lds_bank_conflict_rate", "{:.4f}"),
+              ("VALU active per wave-cycle", "valu_active_per_wave_cycle", "{:.3f}"),
+              ("waiting on LDS per wave-cycle", "lds_wait_per_wave_cycle", "{:.3f}"),
+              ("waiting (any) per wave-cycle", "any_wait_per_wave_cycle", "{:.3f}"),
+              ("SQ_WAIT_ANY per wave-cycle (waitcnt and barrier waits)", "wait_any_per_wave_cycle", "{:.3f}"),
+              ("instruction issued per wave-cycle", "issue_any_per_wave_cycle", "{:.3f}"),
+              ("MFMA cycles with a VALU op co-executing", "valu_mfma_coexec_of_mfma_busy", "{:.3f}"),
+              ("transcendental (exp, log, rcp) per MFMA", "trans_per_mfma", "{:.2f}"),
+              ("LDS FIFO-full cycles per CU-cycle", "lds_fifo_full_per_cu_cycle", "{:.4f}"),
+              ("branches per MFMA", "branches_per_mfma", "{:.3f}"),
+              ("HBM read / write (GB)", None, None),
+              ("HBM bytes / algorithmic bytes", "hbm_ratio_to_algorithmic", "{:.3f}")]
+    for label, key, fmt in fields:
+        cells = []
+        for v in out.values():
+            if label.startswith("duration"):
+                cells.append(f"{v['duration_ms_p1']:.4f} / {v['duration_ms_p2']:.4f}")
+            elif label.startswith("HBM read"):
+                cells.append(f"{v['hbm_read_bytes'] / 1e9:.4f} / {v['hbm_write_bytes'] / 1e9:.4f}")
+            elif key == "kernel":
+                name = v["kernel"]
+                cells.append(f"`{name if len(name) < 90 else name[:87] + '...'}`")
+            else:
+                cells.append(fmt.format(v[key]))
+        lines.append(f"| {label} | " + " | ".join(cells) + " |")
+    lines += ["", "```json", json.dumps(out, indent=1, default=float), "```", ""]
+    print("\n".join(lines))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,7 +446,15 @@ def main() -> int:
                     help="attention workload of the line (the default is the headline the metric names)")
     ap.add_argument("--variant", default=None, choices=["basic", "optimized", "sliced"],
                     help="attention variant (default: the workload's own)")
-    ap.add_argument("--cpu-slices", type=int, default=4)
+    ap.add_argument("--fa-tile", default=None, metavar="BM,BN,WAVES,STAGES",
+                    help="attention tile as the reference's tune arguments (BLOCK_M, BLOCK_N, NUM_WARPS, "
+                         "NUM_STAGES) instead of the tuning table's choice")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the alternating vendor-library timings")
+    ap.add_argument("--counter-run", action="store_true",
+                    help="for rocprofv3 --pmc passes: calibration launches first, then 10 warm-up + 10 timed "
+                         "launches of each kernel, no CPU or vendor legs")
+    ap.add_argument("--counters-summarize", metavar="DIR",
+                    help="summarise the counter passes in DIR (see COUNTER_PASSES) as markdown and exit")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one 256 MiB copy (counter calibration), one attention forward and one GEMM, then exit "
                          "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
@@ -224,6 +463,12 @@ def main() -> int:
     args = ap.parse_args()
     if args.traffic_summarize:
         return _traffic_summarize(*args.traffic_summarize)
+    if args.counters_summarize:
+        return _counters_summarize(args.counters_summarize, args.fa_config, steps=10, fa_tile=args.fa_tile)
+    if args.counter_run:
+        args.steps, args.warmup, args.no_cpu = 10, 10, True
+    # alternating vendor rounds: (rounds, launches per round); fewer under counter collection
+    vendor_rounds = (2, 5) if args.counter_run else (5, 10)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -245,6 +490,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.traffic_probe:
         return _traffic_probe(torch, flash_atten, tuner, mma, dev)
+    if args.counter_run:
+        _calibration_launches(torch, dev)
     limits = hip_lib.device_limits(0)
     _log(f"device gfx{limits['gcn_arch']} CUs={limits['cu_count']} clock={limits['clock_khz'] / 1e6:.2f} GHz")
 
@@ -261,8 +508,16 @@ def main() -> int:
         "optimized": tuner.FlashAttentionOptimizeSharedMemTuner,
         "sliced": tuner.FlashAttentionBlockDNomaskTuner,
     }[variant]
+    tune_args = None
+    if args.fa_tile:
+        bm_, bn_, w_, st_ = (int(x) for x in args.fa_tile.split(","))
+        tune_args = tuner.FlashAttenTuneArguments(BLOCK_M=bm_, BLOCK_N=bn_, BLOCK_N_PAD=bn_, NUM_WARPS=w_,
+                                                  NUM_STAGES=st_)
     spec = tuner_cls(tuple(q.shape), tuple(k.shape), tuple(v.shape), q.element_size(), causal=causal,
-                     return_lse=False).build_flash_attention_launch_spec(q, k, v)
+                     return_lse=False, tune_args=tune_args).build_flash_attention_launch_spec(q, k, v)
+    if tune_args is not None and spec.launch_context.get("tune_args_relaxed"):
+        raise SystemExit(f"--fa-tile {args.fa_tile} is not built for this workload "
+                         f"(relaxed: {spec.launch_context['tune_args_relaxed']})")
     # the reference's FLOP count (test_flash_atten.py:234-240): causal counts N(N+1)/2 scores per (b, h)
     fa_flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
     _log(f"attention {args.fa_config} {variant}: tile {spec.kernel_kwargs['BLOCK_M']}x{spec.kernel_kwargs['BLOCK_N']} "
@@ -288,7 +543,22 @@ def main() -> int:
     p = torch.softmax(sc, dim=-1)
     ref = torch.einsum("rn,rnd->rd", p, vs)
     fa_err = (o.reshape(B * H, N, D)[bh, m].float() - ref).abs().max().item()
-    del q, k, v, spec, o, qs, ks, vs, sc, p, ref
+    del qs, ks, vs, sc, p, ref
+    fa_vendor = None
+    if not args.no_vendor:
+        import torch.nn.functional as F
+
+        med = _alternating(torch, {"ours": lambda: flash_atten.flash_attention(spec),
+                                   "torch_sdpa": lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal)},
+                           rounds=vendor_rounds[0], per_round=4)
+        fa_vendor = {"library": "torch.nn.functional.scaled_dot_product_attention (default ROCm backend)",
+                     "value": round(fa_flops / (med["torch_sdpa"] * 1e-3) / 1e12, 2),
+                     "ours_same_rounds": round(fa_flops / (med["ours"] * 1e-3) / 1e12, 2),
+                     "speedup": round(med["torch_sdpa"] / med["ours"], 3),
+                     "protocol": f"{vendor_rounds[0]} alternating rounds of 4 back-to-back launches each, median "
+                                 "per launch"}
+        _log(f"attention vs torch SDPA: {fa_vendor}")
+    del q, k, v, spec, o
     torch.cuda.empty_cache()
 
     # ---- GEMM ---------------------------------------------------------------------------------------
@@ -310,15 +580,27 @@ def main() -> int:
     ref = a.float() @ b.float()
     gemm_rel = ((c.float() - ref).norm() / ref.norm()).item()
     _log(f"gemm {bm}x{bn}x{bk} waves={warps} group_m={group_m}: {g_total / args.steps:.3f} ms, {gemm_tflops:.1f} TFLOP/s, rel_fro={gemm_rel:.2e}")
-    del a, b, c, ref
+    del ref
+    gemm_vendor = None
+    if not args.no_vendor:
+        med = _alternating(torch, {"ours": gemm, "hipblaslt": lambda: torch.matmul(a, b, out=c)},
+                           rounds=vendor_rounds[0], per_round=vendor_rounds[1])
+        gemm_vendor = {"library": "torch.matmul (hipBLASLt)",
+                       "value": round(gemm_flops / (med["hipblaslt"] * 1e-3) / 1e12, 2),
+                       "ours_same_rounds": round(gemm_flops / (med["ours"] * 1e-3) / 1e12, 2),
+                       "speedup": round(med["hipblaslt"] / med["ours"], 3),
+                       "protocol": f"{vendor_rounds[0]} alternating rounds of {vendor_rounds[1]} back-to-back "
+                                   "launches each, median per launch"}
+        _log(f"gemm vs hipBLASLt: {gemm_vendor}")
+    del a, b, c
     torch.cuda.empty_cache()
 
     # ---- CPU baseline (reference CPU path, bounded sample) ---------------------------------------
     cpu_fa = cpu_gemm = None
     if not args.no_cpu:
-        _log("timing the CPU baseline (bounded sample)")
-        cpu_fa = _cpu_baseline_attention(torch, B, H, N, D, args.cpu_slices, sample_n=512)
-        cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K, sample=(2048, 256, 2048))
+        _log("timing the CPU baseline (the reference's CPU path on this host)")
+        cpu_fa = _cpu_baseline_attention(torch, B, H, N, D)
+        cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K)
 
     traffic = gemm_traffic = None
     if TRAFFIC_FILE.exists():
@@ -361,6 +643,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": 4 * B * H * N * D * 2,
         },
         "cpu_baseline": cpu_fa,
+        "vendor": fa_vendor,
         "parity": {"fa_max_abs_err_64_rows": fa_err, "gemm_rel_fro": gemm_rel},
         "gemm": {
             "metric": "GEMM fp16 TFLOP/s at 8192^3",
@@ -380,6 +663,7 @@ def main() -> int:
                 "algorithmic_bytes_per_launch": 2 * (M * K + K * Ng + M * Ng),
             },
             "cpu_baseline": cpu_gemm,
+            "vendor": gemm_vendor,
         },
     }
     print(json.dumps(line), flush=True)

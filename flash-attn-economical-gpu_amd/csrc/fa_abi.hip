@@ -72,10 +72,11 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 }
 
 // Pipeline of a launch: basic keeps one K/V buffer (1); optimized and sliced double-buffer K/V (2),
-// or, when the tile asks for stages=3, run the software-pipelined kernel (LDS-DMA ring).
+// or, when the tile asks for stages=3 or 4, run a software-pipelined kernel (LDS-DMA ring; 4 = the
+// two-tile-ahead pipeline).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
-  return (t != nullptr && t->stages == 3) ? 3 : 2;
+  return (t != nullptr && (t->stages == 3 || t->stages == 4)) ? t->stages : 2;
 }
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.
@@ -115,7 +116,7 @@ const fa::FaKernelEntry* resolve_fwd(int variant, int dtype, int D, const fa_til
   return e;
 }
 
-// Does the pipelined (stages=3) kernel's addressing hold for this launch? It reads one (batch,
+// Does the pipelined (stages=3 or 4) kernels' addressing hold for this launch? It reads one (batch,
 // kv-head) row range [0, N + block_n) of K and V with 32-bit byte offsets, and its tail check needs
 // whole rows (row stride >= D).
 bool pipelined_fits(const fa_fwd_args* a, int block_n) {
@@ -207,7 +208,7 @@ int fa_fwd_supported(int32_t variant, int32_t dtype, int32_t D, const fa_tile* t
   const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
   if (e == nullptr) return code;
   if (split && find_merge(dtype, D) == nullptr) return fail(FA_ENOTSUP, "no merge kernel for D=%d", D);
-  if (e->stages == 3 && double_buffered_fallback(e) == nullptr)
+  if (e->stages >= 3 && double_buffered_fallback(e) == nullptr)
     return fail(FA_ENOTSUP, "pipelined tile without a double-buffered fallback for D=%d", D);
   return ok();
 }
@@ -234,7 +235,7 @@ static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* st
   if (!std::isfinite(a->sm_scale) || a->sm_scale <= 0.f)
     return fail(FA_EINVAL, "sm_scale must be positive and finite, got %g", (double)a->sm_scale);
 
-  if (e->stages == 3 && !pipelined_fits(a, e->block_n)) {
+  if (e->stages >= 3 && !pipelined_fits(a, e->block_n)) {
     // The pipelined kernel addresses one (batch, kv-head) row range [0, N + block_n) of K and V
     // with 32-bit byte offsets and relies on whole rows for its tail check: run the
     // double-buffered kernel of the same rows per workgroup instead (same block_n where it is

@@ -36,6 +36,8 @@
 //  * GQA: query head h reads KV head h / (H / H_kv); no K/V expansion.
 //  * Split-KV: the SPLIT instantiation writes fp32 normalised partial O and partial LSE per KV
 //    split; fa_merge_kernel combines them: lse = ln sum_j exp(lse_j), O = sum_j exp(lse_j - lse) O_j.
+#include <type_traits>
+
 #include "fa_common.h"
 #include "fa_kernels.h"
 #include "../../include/fa_gfx950.h"
@@ -312,11 +314,13 @@ struct FwdKernel {
   static constexpr int KT_ELEMS = NKB * 512;  // 16-bit elements per K tile
   static constexpr int VT_ELEMS = NVB * 512;
   // Tiles of K (and of V) resident in LDS: 3 when one workgroup owns the CU, 2 when two
-  // four-wave workgroups share it (RT = 1: two waves per SIMD).
-  static constexpr int RING = (WAVES >= 8 || RT >= 2) ? 3 : 2;
+  // four-wave workgroups share it (RT = 1: two waves per SIMD). The stages=4 D = 256 kernel holds
+  // one workgroup per CU (one wave per SIMD) and keeps 3.
+  static constexpr int RING = (WAVES >= 8 || RT >= 2 || (STAGES == 4 && D > 128)) ? 3 : 2;
   static constexpr int NKW = NKB / WAVES;            // DMA blocks per wave per K tile
   static constexpr int NVW = NVB / WAVES;
-  static_assert(STAGES != 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
+  static_assert(STAGES < 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
+  static_assert(STAGES != 4 || RING <= 3, "the stages=4 waits assume a ring of at most 3 tiles");
 
   __device__ static inline void qk_fm(STile& s, const u32x4 (&qf)[RT][DC], const uint16_t* kslot_lane) {
     if constexpr (JT * RT == 1) {
@@ -363,6 +367,98 @@ struct FwdKernel {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) acc[dt][rt] = T::mfma32(vf, pk[kc][rt], acc[dt][rt]);
       }
+    }
+  }
+
+  // ---- stages=4: two-tile-ahead pipeline ----
+  // One step's matrix work: the QK MFMAs of tile u+2 (S^T into `nxt`) and the PV MFMAs of tile u
+  // (O^T += V^T P^T with `pk`), one for one. Both counts are BN * D / 512 per row tile. QK pairs
+  // run score-tile-major, so the second 32-key score tile's accumulators come to life only halfway
+  // through the step (registers: the step also holds S_{u+1}, P_u and P_{u+1}); a QK MFMA then
+  // depends on the QK two MFMAs back, with an independent PV MFMA between them. PV pairs run
+  // key-chunk-major, so P_u's registers die chunk by chunk.
+  static constexpr int NQ = JT * DC;
+  static_assert(NQ == KC * DTL, "QK and PV MFMA counts per tile are equal");
+  __device__ static inline void qk_pv_fm(STile& nxt, const u32x4 (&qf)[RT][DC], const uint16_t* kslot_lane,
+                                         floatx16 (&acc)[DTL][RT], const u32x4 (&pk)[KC][RT],
+                                         const uint16_t* vslot_lane) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nxt[jt][rt][r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int jt = i / DC, cc = i % DC;
+      const int kc = i / DTL, dt = i % DTL;
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(kslot_lane + (jt * DC + cc) * 512);
+      const uint16_t* vb = vslot_lane + (kc * DTL + dt) * 512;
+      const u32x2 lo = lds_read_tr16(vb);
+      const u32x2 hi = lds_read_tr16(vb + 256);
+      const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        nxt[jt][rt] = T::mfma32(kf, qf[rt][cc], nxt[jt][rt]);
+        acc[dt][rt] = T::mfma32(vf, pk[kc][rt], acc[dt][rt]);
+      }
+    }
+  }
+
+  // Online softmax of one (already masked) score tile without a branch: a row whose max grew by
+  // more than THRESH (log2 units) over its exponent offset moves the offset to that max, and its
+  // alpha = exp2((m_old - m_new) c) rescales l now and O once this step's PV is done
+  // (rescale_acc); other rows keep alpha = 1. P and the row sum use the updated offset.
+  __device__ static inline void softmax_nb(const STile& s, u32x4 (&pk)[KC][RT], float (&m_use)[RT],
+                                           float (&l_i)[RT], float (&alpha)[RT], float c, float thr) {
+    float mx[RT];
+    tile_max(s, mx);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const bool up = mx[rt] > m_use[rt] + thr;  // false while the row has seen no key (mx = -inf)
+      const float m_new = up ? mx[rt] : m_use[rt];
+      // one unconditional exp of a selected argument (a conditional exp becomes a divergent branch
+      // that splits the step's block): exp2(0) = 1 for rows that keep their offset, exp2(-inf) = 0
+      // for a row's first finite max
+      alpha[rt] = fast_exp2(up ? (m_use[rt] - m_new) * c : 0.f);
+      l_i[rt] *= alpha[rt];
+      m_use[rt] = m_new;
+    }
+    exp_pack(s, pk, m_use, l_i, c);
+  }
+
+  // O *= alpha per row, when any row of the wave moved its offset (rare).
+  __device__ static inline void rescale_acc(floatx16 (&acc)[DTL][RT], const float (&alpha)[RT]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (__builtin_amdgcn_ballot_w64(alpha[rt] != 1.f) != 0) {
+        pin_acc_agpr(acc, rt);
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][rt][r] *= alpha[rt];
+        pin_acc_agpr(acc, rt);
+      }
+    }
+  }
+
+  // Scheduling of a stages=4 step block: LDS reads a few fragments ahead, then per MFMA one or two
+  // LDS reads and an even share of the softmax VALU work.
+  static constexpr int kSoftValu = JT * RT * (16 * 2 + 8 * 2) + 12 * RT;
+  template <bool WITH_QK>
+  __device__ static inline void step_schedule() {
+    constexpr int mfma = (WITH_QK ? 2 : 1) * NQ;  // groups of RT MFMAs
+    constexpr int valu = (kSoftValu + mfma - 1) / mfma;
+    // QK and PV alternate: 1 K read, then 2 V reads per pair of MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, WITH_QK ? 3 : 2 * kReadAheadV, 3);
+#pragma unroll
+    for (int i = 0; i < mfma / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 3);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 3);
+      __builtin_amdgcn_sched_group_barrier(0x002, valu, 3);
+      __builtin_amdgcn_sched_group_barrier(0x008, RT, 3);
+      __builtin_amdgcn_sched_group_barrier(0x100, WITH_QK ? 1 : 2, 3);
+      __builtin_amdgcn_sched_group_barrier(0x002, valu, 3);
     }
   }
 
@@ -442,6 +538,13 @@ struct FwdKernel {
         qf[rt][cc] = val;
       }
     }
+    if constexpr (STAGES == 4) {
+      // Retire the Q loads here, on every path, before any LDS-DMA is in flight. The compiler does
+      // not see the DMAs (inline asm); where it cannot prove the Q loads were waited for on every
+      // path into the loop it puts a vmcnt(0) before the step's first MFMA, which at run time
+      // waits for the step's own K/V prefetch as well.
+      __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));
+    }
     if constexpr (kAccInAgpr) {
       // Q is only ever an MFMA operand, which may sit in AGPRs: this leaves VGPRs for fragment
       // read-ahead in the one-wave-per-SIMD kernels.
@@ -508,8 +611,8 @@ struct FwdKernel {
           pv_schedule();
         }
       }
-    } else if constexpr (STAGES == 3) {
-      // Software pipeline across KV tiles inside each wave. Step u starts with S_u = K_u Q^T and
+    } else if constexpr (STAGES >= 3) {
+      // stages=3: software pipeline across KV tiles inside each wave. Step u starts with S_u = K_u Q^T and
       // its row max already computed, then
       //   (rare branch) lazy rescale for tile u
       //   X: P_u = exp(S_u)      interleaved with  S_{u+1} = K_{u+1} Q^T      (VALU | MFMA)
@@ -560,6 +663,7 @@ struct FwdKernel {
       };
       const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
       const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
+      if constexpr (STAGES == 3) {
       STile sa, sb;
       float mxa[RT], mxb[RT];
       if (ntiles > 0) {
@@ -630,6 +734,111 @@ struct FwdKernel {
         } else {
           last(sa, mxa, u);
         }
+      }
+      } else {
+      // stages=4: two-tile-ahead pipeline. Before step u the wave holds P_u (packed) and S_{u+1}
+      // (scores); step u is one block of
+      //   MFMA: S_{u+2} = K_{u+2} Q^T  one for one with  O += P_u V_u
+      //   VALU: masks (rare branch before the block), row max, offset update and P_{u+1} = exp(S_{u+1})
+      // so the softmax VALU work spreads evenly over all of the step's MFMAs, none of which waits
+      // on an MFMA of the same step except every other QK of a single score tile. A row whose
+      // offset moved has O rescaled after the block (rare). K runs two tiles ahead of V: step u
+      // reads K_{u+2} and V_u. Rings of RING slots: after the prologue (which reads K_0 and K_1)
+      // K_{RING} and K_{RING+1} refill their slots; step u >= 1 issues K_{u+RING+1} into K_{u+1}'s
+      // slot and V_{u+RING-1} into V_{u-1}'s (both read in step u-1). With RING = 3 those loads
+      // stay in flight across the barrier ending step u (they are read in step u+2 or later).
+      STile s0, s1;                    // scores of even / odd tiles
+      u32x4 p0[KC][RT], p1[KC][RT];    // packed P of even / odd tiles
+      float alpha[RT];
+      const float thr = THRESH / p.c;
+      auto fix_masked4 = [&](STile& cur, int u) {
+        const int n0 = (t_begin + u) * BN;
+        if (tile_needs_mask(n0, wrow0, p)) mask_tile(cur, n0, wrow0, col, hh, p);
+      };
+      if (ntiles > 0) {
+#pragma unroll
+        for (int i = 0; i < RING; ++i) {
+          issue_k(i);
+          issue_v(i);
+        }
+        wait_vm_lds_barrier<0>();
+        if (wave_has_rows) {
+          qk_fm(s0, qf, klane);
+          if (ntiles > 1) qk_fm(s1, qf, klane + KT_ELEMS);
+        }
+        wait_vm_lds_barrier<0>();  // every wave is done with K slots 0 and 1
+        issue_k(RING);
+        issue_k(RING + 1);
+        if (wave_has_rows) {
+          fix_masked4(s0, 0);
+          softmax_nb(s0, p0, m_use, l_i, alpha, p.c, thr);  // O is zero: alpha needs no rescale
+        }
+        // Step 0 reads K_2: with RING = 2 it was just issued (into K_0's slot), so wait for it (K_3,
+        // when issued after it, may stay in flight); with RING = 3 it arrived before the prologue.
+        if constexpr (RING == 2) {
+          if (RING + 1 < ntiles)
+            wait_vm_lds_barrier<NKW>();
+          else
+            wait_vm_lds_barrier<0>();
+        }
+      }
+      // WITH_QK: tile u+2 exists. s_a: S_{u+1} (becomes P_{u+1} in p_n); s_b: receives S_{u+2};
+      // p_c: P_u.
+      auto step4 = [&](auto with_qk, STile& s_a, STile& s_b, u32x4 (&p_c)[KC][RT], u32x4 (&p_n)[KC][RT],
+                       int u) {
+        constexpr bool WITH_QK = decltype(with_qk)::value;
+        const bool full_issue = u >= 1 && u + RING + 1 < ntiles;
+        if (u >= 1) {
+          issue_k(u + RING + 1);  // into K_{u+1}'s slot
+          issue_v(u + RING - 1);  // into V_{u-1}'s slot
+        }
+        if (wave_has_rows) {      // waves without rows still move their share of K/V
+          fix_masked4(s_a, u + 1);
+          if constexpr (WITH_QK)
+            qk_pv_fm(s_b, qf, klane + ((u + 2) % RING) * KT_ELEMS, acc, p_c, vlane + (u % RING) * VT_ELEMS);
+          else
+            pv_fm(acc, p_c, vlane + (u % RING) * VT_ELEMS);
+          softmax_nb(s_a, p_n, m_use, l_i, alpha, p.c, thr);
+          if constexpr (D <= 128) step_schedule<WITH_QK>();
+          // P_{u+1} and l are complete here: without this the compiler sinks their VALU work past
+          // the rescale branch below, out of the MFMA block it is meant to overlap.
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(p_n[kc][rt]));
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(l_i[rt]));
+          rescale_acc(acc, alpha);
+        }
+        // Step u+1 reads K_{u+3} and V_{u+1}: with RING = 3 both were issued before this step.
+        if (RING > 2 && full_issue)
+          wait_vm_lds_barrier<NKW + NVW>();
+        else
+          wait_vm_lds_barrier<0>();
+      };
+      auto last4 = [&](u32x4 (&p_c)[KC][RT], int u) {
+        if (!wave_has_rows) return;
+        pv_fm(acc, p_c, vlane + (u % RING) * VT_ELEMS);
+        pv_schedule();
+      };
+      // Every step runs its QK MFMAs, also when tile u+2 does not exist (the second-to-last step):
+      // that score tile is never used, and it costs one step's QK work per workgroup. A final step
+      // without QK, or the last tile handled inside the loop, raised the kernel's register peak
+      // past the file and made the compiler spill inside the steady-state loop.
+      using QK = std::integral_constant<bool, true>;
+      if (ntiles > 0) {
+        int u = 0;  // even at the top: P_u in p0, S_{u+1} in s1
+        for (; u + 2 < ntiles; u += 2) {
+          step4(QK{}, s1, s0, p0, p1, u);
+          step4(QK{}, s0, s1, p1, p0, u + 1);
+        }
+        if (u + 1 < ntiles) {
+          step4(QK{}, s1, s0, p0, p1, u);
+          last4(p1, u + 1);
+        } else {
+          last4(p0, u);
+        }
+      }
       }
     } else {
       // Double-buffered K/V tiles: tile u is computed from buffer u & 1 while tile u+1 travels
@@ -861,12 +1070,21 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 3, 1)
 
+// Two-tile-ahead pipelined kernels (stages=4).
+#define FA_ENTRIES_PIPE4(TAG, DTYPE, D)                     \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 4, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 4, 1),                  \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 4, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 8, 1, 64, 4, 1)
+
 // D = 256, pipelined with 32-key tiles: Q (64 registers) and O (128) leave room for two 32-key
 // score tiles; a step then has the MFMA count and LDS bytes of a 64-key D = 128 step with half
 // its softmax work per MFMA.
 #define FA_ENTRIES_D256_PIPE(TAG, DTYPE)                    \
   FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 0),                \
-  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 1)
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 1),                \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 4, 0),                \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 4, 1)
 
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),
@@ -875,6 +1093,8 @@ static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D_WIDE(f16_t, FA_DTYPE_F16, 64), FA_ENTRIES_D_WIDE(f16_t, FA_DTYPE_F16, 128),
     FA_ENTRIES_D_WIDE(bf16_t, FA_DTYPE_BF16, 64), FA_ENTRIES_D_WIDE(bf16_t, FA_DTYPE_BF16, 128),
     FA_ENTRIES_D256_PIPE(f16_t, FA_DTYPE_F16), FA_ENTRIES_D256_PIPE(bf16_t, FA_DTYPE_BF16),
+    FA_ENTRIES_PIPE4(f16_t, FA_DTYPE_F16, 64),  FA_ENTRIES_PIPE4(f16_t, FA_DTYPE_F16, 128),
+    FA_ENTRIES_PIPE4(bf16_t, FA_DTYPE_BF16, 64), FA_ENTRIES_PIPE4(bf16_t, FA_DTYPE_BF16, 128),
 };
 
 static const FaMergeEntry kMergeEntries[] = {
