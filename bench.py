@@ -34,8 +34,10 @@ for _p in (str(PKG), str(ROOT)):
 
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16/bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on `--traffic-probe`.
-TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_fa_b4h32n8192d128_gemm8192.json"
+# HBM bytes per launch of each attention workload and of the 8192^3 GEMM, from rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE passes over this script's own warmed launches (`--counters-summarize
+# ... --traffic-out`).
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_fa_fwd_configs_gemm8192.json"
 SEED = 20260328  # the reference's constant (test_flash_atten.py:33)
 FA_SHAPE = dict(B=4, H=32, N=8192, D=128)
 # Attention workloads of the BASELINE configurations: the headline (default line) and, for
@@ -177,88 +179,6 @@ def _alternating(torch, fns: dict, rounds: int, per_round: int) -> dict:
     return {name: statistics.median(v) for name, v in times.items()}
 
 
-def _traffic_probe(torch, flash_atten, tuner, mma, dev) -> int:
-    """One dispatch each of: a 256 MiB fp32 copy (known bytes, calibrates the counters), the headline
-    attention forward, and the 8192^3 GEMM."""
-    g = torch.Generator().manual_seed(SEED)
-    src = torch.randn(64 * 1024 * 1024, generator=g).to(dev)
-    torch.empty_like(src).copy_(src)
-    torch.cuda.synchronize()
-    del src
-    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
-    q, k, v = (torch.randn(B, H, N, D, generator=g, dtype=torch.float16).to(dev) for _ in range(3))
-    spec = tuner.FlashAttentionOptimizeSharedMemTuner(tuple(q.shape), tuple(k.shape), tuple(v.shape), 2, causal=False,
-                                                      return_lse=False).build_flash_attention_launch_spec(q, k, v)
-    flash_atten.flash_attention(spec)
-    torch.cuda.synchronize()
-    del q, k, v, spec
-    M, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
-    a = (torch.rand(M, K, generator=g) * 2 - 1).half().to(dev)
-    b = (torch.rand(K, Ng, generator=g) * 2 - 1).half().to(dev)
-    mma.matmul(a, b)
-    torch.cuda.synchronize()
-    _log("traffic probe done")
-    return 0
-
-
-TRAFFIC_COMMAND = (
-    "export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/traffic -o fetch -- "
-    "python -u bench.py --traffic-probe && rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/traffic "
-    "-o write -- python -u bench.py --traffic-probe && python bench.py --traffic-summarize "
-    "gpurun_out/traffic/fetch_counter_collection.csv gpurun_out/traffic/write_counter_collection.csv"
-)
-
-
-def _traffic_summarize(fetch_csv: str, write_csv: str, out_path: Path = TRAFFIC_FILE) -> int:
-    """Write TRAFFIC_FILE from the two counter passes over --traffic-probe. FETCH_SIZE and WRITE_SIZE
-    are KiB per dispatch (summed over the counter instances); each is scaled by the factor that
-    makes the calibration copy read/write exactly its 256 MiB."""
-    import csv
-
-    def per_dispatch(path: str) -> list[tuple[str, float]]:
-        acc: dict[int, list] = {}
-        with open(path) as fh:
-            for r in csv.DictReader(fh):
-                d = int(r["Dispatch_Id"])
-                acc.setdefault(d, [r["Kernel_Name"], 0.0])[1] += float(r["Counter_Value"])
-        return [tuple(acc[d]) for d in sorted(acc)]
-
-    fetch, write = per_dispatch(fetch_csv), per_dispatch(write_csv)
-
-    def pick(rows, needle):
-        hits = [v for name, v in rows if needle in name]
-        if not hits:
-            raise SystemExit(f"no dispatch matching {needle!r}")
-        return hits[-1]
-
-    copy_bytes = 64 * 1024 * 1024 * 4
-    f_copy = next(v for name, v in fetch if "fa_fwd" not in name and "gemm" not in name)
-    w_copy = next(v for name, v in write if "fa_fwd" not in name and "gemm" not in name)
-    f_factor = round(copy_bytes / (f_copy * 1024), 2)
-    w_factor = round(copy_bytes / (w_copy * 1024), 2)
-    B, H, N, D = FA_SHAPE["B"], FA_SHAPE["H"], FA_SHAPE["N"], FA_SHAPE["D"]
-    M, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
-    out = {
-        "command": TRAFFIC_COMMAND,
-        "note": ("Two counter passes over `bench.py --traffic-probe`: one 256 MiB fp32 copy (calibration), one "
-                 "attention forward (optimized variant through the tuner, fp16 B=4 H=32 N=8192 D=128 non-causal), "
-                 "one fp16 GEMM 8192^3 (tile from the tuning table). Counter values are KiB per dispatch; bytes = "
-                 "value x 1024 x factor."),
-        "calibration": {"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes, "FETCH_SIZE_KiB": f_copy,
-                        "WRITE_SIZE_KiB": w_copy, "fetch_factor": f_factor, "write_factor": w_factor},
-    }
-    for key, needle, algo in (("fa_fwd_b4h32n8192d128_f16", "fa_fwd", 4 * B * H * N * D * 2),
-                              ("gemm_f16_8192cube", "gemm", 2 * (M * K + K * Ng + M * Ng))):
-        fk, wk = pick(fetch, needle), pick(write, needle)
-        rd, wr = int(fk * 1024 * f_factor), int(wk * 1024 * w_factor)
-        out[key] = {"FETCH_SIZE_KiB": fk, "WRITE_SIZE_KiB": wk, "bytes_read": rd, "bytes_written": wr,
-                    "bytes_per_launch": rd + wr, "algorithmic_bytes_per_launch": algo,
-                    "ratio_to_algorithmic": round((rd + wr) / algo, 4)}
-    Path(out_path).write_text(json.dumps(out, indent=2) + "\n")
-    print(json.dumps(out, indent=2))
-    return 0
-
-
 # Counter passes for `--counters-summarize` (each within one pass's hardware limits: at most 8 SQ,
 # 4 TCC and 2 GRBM counters). Each pass profiles one `bench.py --counter-run` process.
 COUNTER_PASSES = {
@@ -295,7 +215,8 @@ def _calibration_launches(torch, dev) -> None:
     torch.cuda.empty_cache()
 
 
-def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str | None = None) -> int:
+def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str | None = None,
+                        traffic_out: str | None = None) -> int:
     """Markdown summary of the counter passes over `bench.py --counter-run --fa-config <cfg>`: per
     kernel, the mean over its last `steps` dispatches (the bench's timed launches, after its
     warm-up), clock and MFMA utilisation, instruction mix, LDS conflicts and calibrated HBM bytes."""
@@ -431,6 +352,23 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
         lines.append(f"| {label} | " + " | ".join(cells) + " |")
     lines += ["", "```json", json.dumps(out, indent=1, default=float), "```", ""]
     print("\n".join(lines))
+    if traffic_out:
+        path = Path(traffic_out)
+        doc = json.loads(path.read_text()) if path.exists() else {}
+        doc["note"] = ("HBM bytes per launch: FETCH_SIZE x 1024 x fetch_factor + WRITE_SIZE x 1024 x write_factor, means "
+                       "over the bench's timed launches under rocprofv3 --pmc; the factors make out = in + 1 over fp32 "
+                       f"tensors of {', '.join(f'{m} MiB' for m in CALIBRATION_MIB)} read and write exactly their size.")
+        doc[f"calibration_{fa_config}"] = {"fetch_factor": round(f_factor, 4), "write_factor": round(w_factor, 4),
+                                           "fetch_factors_per_size": [round(x, 4) for x in f_factors],
+                                           "write_factors_per_size": [round(x, 4) for x in w_factors]}
+        for key, name in (("attention", f"fa_fwd_{fa_config}"), ("gemm", "gemm_f16_8192cube")):
+            v = out[key]
+            rd_b, wr_b = int(v["hbm_read_bytes"]), int(v["hbm_write_bytes"])
+            doc[name] = {"kernel": v["kernel"], "command": counters_command(fa_config, directory, fa_tile),
+                         "bytes_read": rd_b, "bytes_written": wr_b, "bytes_per_launch": rd_b + wr_b,
+                         "algorithmic_bytes_per_launch": v["algorithmic_bytes"],
+                         "ratio_to_algorithmic": round(v["hbm_ratio_to_algorithmic"], 4)}
+        path.write_text(json.dumps(doc, indent=2, sort_keys=True) + "\n")
     return 0
 
 
@@ -455,16 +393,13 @@ def main() -> int:
                          "launches of each kernel, no CPU or vendor legs")
     ap.add_argument("--counters-summarize", metavar="DIR",
                     help="summarise the counter passes in DIR (see COUNTER_PASSES) as markdown and exit")
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="run one 256 MiB copy (counter calibration), one attention forward and one GEMM, then exit "
-                         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
-    ap.add_argument("--traffic-summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="turn the two counter passes into the HBM traffic table read by the bench line")
+    ap.add_argument("--traffic-out", metavar="JSON",
+                    help="with --counters-summarize: also record the HBM bytes per launch in this file (the bench "
+                         "line's roofline.traffic reads profiles/hbm_traffic_fa_fwd_configs_gemm8192.json)")
     args = ap.parse_args()
-    if args.traffic_summarize:
-        return _traffic_summarize(*args.traffic_summarize)
     if args.counters_summarize:
-        return _counters_summarize(args.counters_summarize, args.fa_config, steps=10, fa_tile=args.fa_tile)
+        return _counters_summarize(args.counters_summarize, args.fa_config, steps=10, fa_tile=args.fa_tile,
+                                   traffic_out=args.traffic_out)
     if args.counter_run:
         args.steps, args.warmup, args.no_cpu = 10, 10, True
     # alternating vendor rounds: (rounds, launches per round); fewer under counter collection
@@ -488,8 +423,6 @@ def main() -> int:
     import tuner
 
     dev = torch.device("cuda:0")
-    if args.traffic_probe:
-        return _traffic_probe(torch, flash_atten, tuner, mma, dev)
     if args.counter_run:
         _calibration_launches(torch, dev)
     limits = hip_lib.device_limits(0)
@@ -603,12 +536,11 @@ def main() -> int:
         cpu_gemm = _cpu_baseline_gemm(torch, M, Ng, K)
 
     traffic = gemm_traffic = None
-    if TRAFFIC_FILE.exists():
+    if TRAFFIC_FILE.exists() and not args.fa_tile and args.variant is None:
         try:
             recorded = json.loads(TRAFFIC_FILE.read_text())
-            # the counter passes cover the headline launch only
-            if args.fa_config == "headline" and variant == "optimized":
-                traffic = recorded.get("fa_fwd_b4h32n8192d128_f16", {}).get("bytes_per_launch")
+            # recorded for each workload's own variant and tuned tile
+            traffic = recorded.get(f"fa_fwd_{args.fa_config}", {}).get("bytes_per_launch")
             gemm_traffic = recorded.get("gemm_f16_8192cube", {}).get("bytes_per_launch")
         except (ValueError, OSError):
             traffic = gemm_traffic = None

@@ -45,7 +45,6 @@ FA_TILE_SPACE = [
     (256, 64, 8, 3),
     (128, 32, 4, 3),
     (128, 64, 4, 4),
-    (256, 64, 8, 4),
     (128, 32, 4, 4),
     (256, 64, 8, 2),
     (256, 64, 4, 2),

@@ -29,9 +29,8 @@ TILES = {
     "pipe128": (OPT, 128, 64, 4, 3),
     "pipe256": (OPT, 256, 64, 8, 3),
     "pipe128n32": (OPT, 128, 32, 4, 3),  # D = 256 pipelined (32-key tiles)
-    # two-tile-ahead pipeline (stages=4): ring of 2 tiles (4 waves) or 3 (8 waves, D = 256)
+    # two-tile-ahead pipeline (stages=4): ring of 2 tiles (D <= 128) or 3 (D = 256)
     "pipe4_128": (OPT, 128, 64, 4, 4),
-    "pipe4_256": (OPT, 256, 64, 8, 4),
     "pipe4_128n32": (OPT, 128, 32, 4, 4),
 }
 
@@ -85,12 +84,12 @@ CASES = [
     ("pipe4_d128", 1, 2, 2, 512, 512, 128, F16, False, "pipe4_128"),
     ("pipe4_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "pipe4_128"),
     ("pipe4_d64", 2, 2, 2, 256, 448, 64, F16, False, "pipe4_128"),
-    ("pipe4_w8_d128_causal", 2, 2, 2, 512, 512, 128, F16, True, "pipe4_256"),
-    ("pipe4_w8_d64_bf16", 1, 3, 3, 256, 576, 64, BF16, False, "pipe4_256"),
+    ("pipe4_d128_causal_b2", 2, 2, 2, 512, 512, 128, F16, True, "pipe4_128"),
+    ("pipe4_d64_bf16", 1, 3, 3, 256, 576, 64, BF16, False, "pipe4_128"),
     ("pipe4_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "pipe4_128"),
     ("pipe4_ragged", 2, 3, 3, 200, 333, 128, F16, False, "pipe4_128"),
-    ("pipe4_w8_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "pipe4_256"),
-    ("pipe4_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pipe4_256"),
+    ("pipe4_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "pipe4_128"),
+    ("pipe4_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pipe4_128"),
     ("pipe4_d256_bf16", 1, 2, 2, 256, 300, 256, BF16, False, "pipe4_128n32"),
     ("pipe4_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "pipe4_128n32"),
     ("pipe4_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "pipe4_128n32"),
@@ -98,14 +97,15 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_256"])
+@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32"])
 @pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320, 384, 448, 512])
 def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     """1..8 KV tiles: the pipelined loops' prologues, unrolled pairs, peeled tails (stages=4: 1, 2
     or 3 trailing steps) and the LDS-DMA rings (2 or 3 slots) at every length parity, with a
     partial last tile."""
     print(f"[fa_abi] pipelined tile counts {tile_name} N={n}", flush=True)
-    B, H, M, D = 1, 2, 96, 128
+    B, H, M = 1, 2, 96
+    D = 256 if TILES[tile_name][2] == 32 else 128  # 32-key tiles are the D = 256 ones
     q, k, v = make_qkv(300 + n, B, H, H, M, n, D, F16)
     o, lse = run_fa(q, k, v, variant=None, tile=TILES[tile_name], causal=False)
     o_ref, lse_ref = oracle.attention(q, k, v, causal=False)
@@ -139,7 +139,7 @@ def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
     B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, BF16
     print(f"[fa_abi] sliced pipelined splits={splits} causal={causal}", flush=True)
     q, k, v = make_qkv(78, B, H, Hkv, M, N, D, dtype)
-    for tile_name in ("pipe128", "pipe256", "pipe4_128", "pipe4_256"):
+    for tile_name in ("pipe128", "pipe256", "pipe4_128"):
         o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES[tile_name], causal=causal, dtype=dtype, splits=splits)
         o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
         assert max_abs(o, o_ref) <= ATOL[dtype], tile_name
