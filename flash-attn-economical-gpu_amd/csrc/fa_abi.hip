@@ -76,7 +76,7 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 // two-tile-ahead pipeline).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
-  return (t != nullptr && (t->stages == 3 || t->stages == 4)) ? t->stages : 2;
+  return (t != nullptr && (t->stages == 3 || t->stages == 4 || t->stages == 5)) ? t->stages : 2;
 }
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.

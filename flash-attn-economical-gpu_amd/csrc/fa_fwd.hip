@@ -180,7 +180,14 @@ struct FwdKernel {
   // rescale needs O in VGPRs; pinning O to AGPRs on both sides of it keeps the AGPR <-> VGPR copies
   // inside the rescale branch. Without the pins the compiler hoisted them to the loop header, where
   // 144 v_accvgpr_read ran on every step of the D = 256 kernel (~15% of its time).
-  static constexpr bool kAccInAgpr = RT > 1 || D > 128;  // more than 256 registers per lane
+  // more than 256 registers per lane (the stages=5 kernel is built to fit 256: O and Q in VGPRs)
+  static constexpr bool kAccInAgpr = (RT > 1 || D > 128) && STAGES != 5;
+  // Workgroups per CU the launch bounds ask for: four-wave workgroups with RT = 1 and D <= 128 (and
+  // the lean stages=5 kernels) fit two per CU; the lean kernel with 32-key D <= 128 tiles fits three.
+  static constexpr int kBlocksPerCu =
+      (WAVES == 4 && RT == 1 && STAGES == 5 && D <= 128 && BN == 32) ? 3
+      : (WAVES == 4 && RT == 1 && (D <= 128 || STAGES == 5))          ? 2
+                                                                       : 1;
   __device__ static inline void pin_acc_agpr(floatx16 (&acc)[DTL][RT], int rt) {
     if constexpr (kAccInAgpr) {
 #pragma unroll
@@ -316,16 +323,18 @@ struct FwdKernel {
   // Tiles of K (and of V) resident in LDS: 3 when one workgroup owns the CU, 2 when two
   // four-wave workgroups share it (RT = 1: two waves per SIMD). The stages=4 D = 256 kernel holds
   // one workgroup per CU (one wave per SIMD) and keeps 3.
-  static constexpr int RING = (WAVES >= 8 || RT >= 2 || (STAGES == 4 && D > 128)) ? 3 : 2;
+  static constexpr int RING = (STAGES == 5) ? 2 : (WAVES >= 8 || RT >= 2 || (STAGES == 4 && D > 128)) ? 3 : 2;
   static constexpr int NKW = NKB / WAVES;            // DMA blocks per wave per K tile
   static constexpr int NVW = NVB / WAVES;
   static_assert(STAGES < 3 || (NKB % WAVES == 0 && NVB % WAVES == 0), "tile blocks must split evenly over waves");
   static_assert(STAGES != 4 || RING <= 3, "the stages=4 waits assume a ring of at most 3 tiles");
 
   __device__ static inline void qk_fm(STile& s, const u32x4 (&qf)[RT][DC], const uint16_t* kslot_lane) {
-    if constexpr (JT * RT == 1) {
+    if constexpr (JT * RT == 1 && STAGES != 5) {
       // A single score tile (D = 256 with 32-key tiles) would be one chain of DC dependent MFMAs:
       // run the even and odd d chunks as two independent chains and add them (+1.5% at D = 256).
+      // The stages=5 kernel has no registers for the second chain; its second wave per SIMD
+      // covers the chain's latency instead.
       floatx16 s0 = {}, s1 = {};
 #pragma unroll
       for (int cc = 0; cc < DC; cc += 2) {
@@ -735,7 +744,7 @@ struct FwdKernel {
           last(sa, mxa, u);
         }
       }
-      } else {
+      } else if constexpr (STAGES == 4) {
       // stages=4: two-tile-ahead pipeline. Before step u the wave holds P_u (packed) and S_{u+1}
       // (scores); step u is one block of
       //   MFMA: S_{u+2} = K_{u+2} Q^T  one for one with  O += P_u V_u
@@ -839,6 +848,33 @@ struct FwdKernel {
           last4(p0, u);
         }
       }
+      } else {
+      // stages=5: one KV tile per step, no cross-tile pipeline inside the wave. The wave holds one
+      // score tile and reads fragments only a little ahead, so O and Q fit in its 256 registers
+      // beside them (D = 256: 128 + 64) and two workgroups share a CU: the other workgroup's wave
+      // on the same SIMD runs its MFMAs while this one does its softmax or waits at its barrier.
+      // Tiles reach LDS by LDS-DMA into a 2-slot ring: step u issues tile u+1 into the slot tile
+      // u-1 left (read in step u-1) and waits for it at the end of the step.
+      static_assert(RING == 2, "stages=5 alternates two ring slots");
+      if (ntiles > 0) {
+        issue_k(0);
+        issue_v(0);
+        wait_vm_lds_barrier<0>();
+      }
+      for (int u = 0; u < ntiles; ++u) {
+        issue_k(u + 1);
+        issue_v(u + 1);
+        if (wave_has_rows) {  // waves without rows still move their share of K/V
+          STile s;
+          u32x4 pk[KC][RT];
+          qk_fm(s, qf, klane + (u & 1) * KT_ELEMS);
+          qk_schedule();
+          softmax(s, pk, acc, m_use, l_i, (t_begin + u) * BN, wrow0, col, hh, p);
+          pv_fm(acc, pk, vlane + (u & 1) * VT_ELEMS);
+          pv_schedule();
+        }
+        wait_vm_lds_barrier<0>();
+      }
       }
     } else {
       // Double-buffered K/V tiles: tile u is computed from buffer u & 1 while tile u+1 travels
@@ -918,9 +954,9 @@ struct FwdKernel {
 };
 
 template <typename Tag, int D, int WAVES, int RT, int BN, int STAGES, bool SPLIT>
-// Four-wave workgroups with RT=1 and D <= 128 fit in 256 registers per lane, so two independent
-// workgroups share a CU (two waves per SIMD); their barriers only align four waves each.
-__global__ __launch_bounds__(WAVES * 64, (WAVES == 4 && RT == 1 && D <= 128) ? 2 : 1) void fa_fwd_kernel(
+// Workgroups per CU from kBlocksPerCu: independent workgroups sharing a CU align only their own
+// waves at their barriers.
+__global__ __launch_bounds__(WAVES * 64, (FwdKernel<Tag, D, WAVES, RT, BN, STAGES, SPLIT>::kBlocksPerCu)) void fa_fwd_kernel(
     FwdParams p) {
   FwdKernel<Tag, D, WAVES, RT, BN, STAGES, SPLIT>::run(p);
 }
@@ -1076,6 +1112,14 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 4, 0),                  \
   FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 4, 1)
 
+// Lean one-tile-per-step kernels (stages=5): 64-key tiles at two workgroups per CU, 32-key tiles at
+// three (D = 128) or more (D = 64).
+#define FA_ENTRIES_LEAN(TAG, DTYPE, D)                      \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 5, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 64, 5, 1),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 32, 5, 0),                  \
+  FA_ENTRY(TAG, DTYPE, D, 4, 1, 32, 5, 1)
+
 // D = 256, pipelined with 32-key tiles: Q (64 registers) and O (128) leave room for two 32-key
 // score tiles; a step then has the MFMA count and LDS bytes of a 64-key D = 128 step with half
 // its softmax work per MFMA.
@@ -1083,7 +1127,9 @@ __global__ __launch_bounds__(256) void fa_merge_kernel(MergeParams p) {
   FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 0),                \
   FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 3, 1),                \
   FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 4, 0),                \
-  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 4, 1)
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 4, 1),                \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 5, 0),                \
+  FA_ENTRY(TAG, DTYPE, 256, 4, 1, 32, 5, 1)
 
 static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 64),    FA_ENTRIES_D(f16_t, FA_DTYPE_F16, 128),
@@ -1094,6 +1140,8 @@ static const FaKernelEntry kFwdEntries[] = {
     FA_ENTRIES_D256_PIPE(f16_t, FA_DTYPE_F16), FA_ENTRIES_D256_PIPE(bf16_t, FA_DTYPE_BF16),
     FA_ENTRIES_PIPE4(f16_t, FA_DTYPE_F16, 64),  FA_ENTRIES_PIPE4(f16_t, FA_DTYPE_F16, 128),
     FA_ENTRIES_PIPE4(bf16_t, FA_DTYPE_BF16, 64), FA_ENTRIES_PIPE4(bf16_t, FA_DTYPE_BF16, 128),
+    FA_ENTRIES_LEAN(f16_t, FA_DTYPE_F16, 64),   FA_ENTRIES_LEAN(f16_t, FA_DTYPE_F16, 128),
+    FA_ENTRIES_LEAN(bf16_t, FA_DTYPE_BF16, 64), FA_ENTRIES_LEAN(bf16_t, FA_DTYPE_BF16, 128),
 };
 
 static const FaMergeEntry kMergeEntries[] = {

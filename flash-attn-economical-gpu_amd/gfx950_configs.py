@@ -38,14 +38,18 @@ VARIANT_BY_KERNEL = {
 #   3  software-pipelined (QK of tile u+1 overlapped with the softmax of tile u inside each wave,
 #      K/V brought into an LDS ring by LDS-DMA loads),
 #   4  two-tile-ahead pipeline (QK of tile u+2 one for one with PV of tile u, the softmax of tile
-#      u+1 spread over both; same LDS-DMA rings).
-# The basic variant uses stages 1; optimized and sliced use 4, 3 or 2.
+#      u+1 spread over both; same LDS-DMA rings),
+#   5  one tile per step in a 2-slot LDS-DMA ring, lean enough in registers for two waves per
+#      SIMD at D = 256.
+# The basic variant uses stages 1; optimized and sliced use 5, 4, 3 or 2.
 FA_TILE_SPACE = [
     (128, 64, 4, 3),
     (256, 64, 8, 3),
     (128, 32, 4, 3),
     (128, 64, 4, 4),
     (128, 32, 4, 4),
+    (128, 32, 4, 5),
+    (128, 64, 4, 5),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),
@@ -63,8 +67,8 @@ FA_TILE_SPACE = [
 ]
 STAGES_BY_VARIANT = {
     hip_lib.FA_VARIANT_BASIC: (1,),
-    hip_lib.FA_VARIANT_OPT: (3, 4, 2),
-    hip_lib.FA_VARIANT_SLICED: (3, 4, 2),
+    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 2),
+    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 2),
 }
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).

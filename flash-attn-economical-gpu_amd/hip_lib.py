@@ -372,7 +372,7 @@ def fwd_kernel_symbol(variant: int, dtype: torch.dtype, D: int, tile: FaTile) ->
     """Mangled name of the attention instantiation a tile resolves to (as in kernel_resources.json)."""
     tag = {torch.float16: "5f16_t", torch.bfloat16: "6bf16_t"}[dtype]
     # the pipeline the C ABI resolves (stages_of in csrc/fa_abi.hip)
-    stages = 1 if variant == FA_VARIANT_BASIC else (tile.stages if tile.stages in (3, 4) else 2)
+    stages = 1 if variant == FA_VARIANT_BASIC else (tile.stages if tile.stages in (3, 4, 5) else 2)
     rows = tile.block_m // tile.waves
     rt = rows // 32
     split = "1" if (variant == FA_VARIANT_SLICED and tile.splits > 1) else "0"

@@ -32,6 +32,8 @@ TILES = {
     # two-tile-ahead pipeline (stages=4): ring of 2 tiles (D <= 128) or 3 (D = 256)
     "pipe4_128": (OPT, 128, 64, 4, 4),
     "pipe4_128n32": (OPT, 128, 32, 4, 4),
+    # one tile per step, two waves per SIMD (stages=5; D = 256)
+    "lean128n32": (OPT, 128, 32, 4, 5),
 }
 
 
@@ -94,10 +96,14 @@ CASES = [
     ("pipe4_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "pipe4_128n32"),
     ("pipe4_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "pipe4_128n32"),
     ("pipe4_d256_long_causal", 1, 2, 2, 700, 700, 256, BF16, True, "pipe4_128n32"),
+    ("lean_d256_bf16", 1, 2, 2, 256, 300, 256, BF16, False, "lean128n32"),
+    ("lean_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "lean128n32"),
+    ("lean_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "lean128n32"),
+    ("lean_d256_long_causal_gqa", 1, 4, 2, 700, 700, 256, BF16, True, "lean128n32"),
 ]
 
 
-@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32"])
+@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32", "lean128n32"])
 @pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320, 384, 448, 512])
 def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     """1..8 KV tiles: the pipelined loops' prologues, unrolled pairs, peeled tails (stages=4: 1, 2
@@ -216,7 +222,8 @@ def _strided_kv(x: np.ndarray, row_stride: int, dtype, device) -> torch.Tensor:
 
 @pytest.mark.parametrize("why", ["short_row_stride", "span_over_4gib"])
 @pytest.mark.parametrize("D,tile_name,dtype", [(128, "pipe128", F16), (256, "pipe128n32", BF16),
-                                               (128, "pipe4_128", F16), (256, "pipe4_128n32", BF16)])
+                                               (128, "pipe4_128", F16), (256, "pipe4_128n32", BF16),
+                                               (256, "lean128n32", BF16)])
 @pytest.mark.parametrize("splits", [1, 2])
 def test_fa_pipelined_fallback(gpu, why, D, tile_name, dtype, splits):
     """A pipelined (stages=3) tile whose addressing rules a launch breaks runs the double-buffered
