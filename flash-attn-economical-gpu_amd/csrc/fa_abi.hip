@@ -400,30 +400,54 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   return ok();
 }
 
+// The built kernel an (op, variant, dtype, D, tile) or GEMM tile resolves to: its function, mangled
+// symbol and workgroup size (shared by fa_kernel_resources and fa_kernel_symbol).
+static int resolve_kernel(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
+                          const gemm_tile* gtile, const void** fn, const char** symbol, int* threads) {
+  if (op == 0) {
+    bool split = false;
+    int code = FA_OK;
+    const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
+    if (e == nullptr) return code;
+    *fn = e->fn;
+    *symbol = e->symbol;
+    *threads = e->waves * 64;
+  } else if (op == 1) {
+    if (gtile == nullptr) return fail(FA_EINVAL, "null gemm tile");
+    const fa::GemmKernelEntry* e = find_gemm(gtile);
+    if (e == nullptr) return fail(FA_ENOTSUP, "gemm tile not built");
+    *fn = e->fn;
+    *symbol = e->symbol;
+    *threads = e->waves * 64;
+  } else {
+    return fail(FA_EINVAL, "unknown op %d", op);
+  }
+  return FA_OK;
+}
+
+int fa_kernel_symbol(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
+                     const gemm_tile* gtile, char* buf, int32_t buf_bytes) {
+  if (buf == nullptr || buf_bytes <= 0) return fail(FA_EINVAL, "null or empty output buffer");
+  const void* fn = nullptr;
+  const char* symbol = nullptr;
+  int threads = 0;
+  const int code = resolve_kernel(op, variant, dtype, D, tile, gtile, &fn, &symbol, &threads);
+  if (code != FA_OK) return code;
+  const size_t n = std::strlen(symbol);
+  if ((int64_t)n + 1 > (int64_t)buf_bytes)
+    return fail(FA_EINVAL, "a %d-byte buffer cannot hold the %zu-byte symbol", buf_bytes, n + 1);
+  std::memcpy(buf, symbol, n + 1);
+  return ok();
+}
+
 int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
                         const gemm_tile* gtile, fa_resources* out) {
   if (out == nullptr) return fail(FA_EINVAL, "null output");
   const void* fn = nullptr;
   const char* symbol = nullptr;
   int threads = 0;
-  if (op == 0) {
-    bool split = false;
-    int code = FA_OK;
-    const fa::FaKernelEntry* e = resolve_fwd(variant, dtype, D, tile, &split, &code);
-    if (e == nullptr) return code;
-    fn = e->fn;
-    symbol = e->symbol;
-    threads = e->waves * 64;
-  } else if (op == 1) {
-    if (gtile == nullptr) return fail(FA_EINVAL, "null gemm tile");
-    const fa::GemmKernelEntry* e = find_gemm(gtile);
-    if (e == nullptr) return fail(FA_ENOTSUP, "gemm tile not built");
-    fn = e->fn;
-    symbol = e->symbol;
-    threads = e->waves * 64;
-  } else {
-    return fail(FA_EINVAL, "unknown op %d", op);
-  }
+  const int code = resolve_kernel(op, variant, dtype, D, tile, gtile, &fn, &symbol, &threads);
+  if (code != FA_OK) return code;
   const fa::KernelResourceRow* row = find_resource_row(symbol);
   if (row == nullptr) return fail(FA_ENOTSUP, "no compiler resource row for %s (stale build)", symbol);
   hipFuncAttributes attr;

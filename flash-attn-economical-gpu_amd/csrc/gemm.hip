@@ -7,8 +7,12 @@
 // with K % 8 == 0 and N % 4 == 0 runs.
 //
 // gfx950 design:
-//  * v_mfma_f32_32x32x16_f16 computes C^T = B^T A^T per 32x32 tile, so the accumulator gives each
-//    lane four consecutive output columns of one row (8-byte stores).
+//  * C^T = B^T A^T per MFMA tile, so the accumulator gives each lane four consecutive output
+//    columns of one row (8-byte stores). Two MFMA shapes, chosen per tile in the registry:
+//    v_mfma_f32_32x32x16_f16 and v_mfma_f32_16x16x32_f16. The 16x16x32 form moves half the
+//    accumulator registers per flop; on MI355X it draws less power per flop, so the power-capped
+//    8-wave tiles run at a higher clock with it (about 1.8 instead of 1.5-1.6 GHz at the same MFMA
+//    occupancy, measured with GRBM_GUI_ACTIVE / SQ_VALU_MFMA_BUSY_CYCLES).
 //  * K slabs (BK deep) reach LDS by LDS-DMA (buffer_load_dwordx4 ... lds), no staging registers,
 //    into a ring of RING slabs: slab s is requested RING-1 slabs before it is multiplied, and the
 //    barrier ending a slab waits only for the next slab's loads (vmcnt), not for the newer ones.
@@ -16,18 +20,25 @@
 //    whole rows: 1024 / (2 BK) rows of A or 1024 / (2 BN) rows of B. Reads are made conflict-free by
 //    XOR-swizzling the 16-byte chunks of each row (the DMA lane that fills slot s fetches logical
 //    chunk s ^ f(row); a lane reading logical chunk c looks at slot c ^ f(row)):
-//      A (row pitch 2 BK = 64 or 128 bytes): f(r) = (r / rows-per-256-bytes) & (chunks - 1), so the
-//        16 rows one ds_read_b128 cycle touches land on 16 distinct 16-byte bank groups;
-//      B (row pitch 2 BN >= 128 bytes): f(k) = 4 ((k / rows-per-256-bytes) & (QB - 1)), so the 4 rows
-//        x 64 bytes of a ds_read_b64_tr_b16 cycle land on distinct bank groups.
-//    Per lane the swizzled addresses reduce to a few registers (one per 16-deep chunk for A, one per
-//    32-column tile for B) plus immediate offsets.
-//  * The MFMA B operand (A^T columns) is one ds_read_b128 per lane; the MFMA A operand (B^T rows, 8
-//    consecutive k per lane) comes from two transposing reads ds_read_b64_tr_b16 of B kept as [k][n]:
-//    in each 16-lane group, lane L addresses row k0 + (L >> 2) at columns n0 + 4 (L & 3), and result
-//    lane i then holds B[k0 + e][n0 + i] for e = 0..3. No register shuffles.
-//  * LDS fragment reads for the next 16-deep chunk are issued while the current chunk's MFMAs run
-//    (scheduling-group hints).
+//      A (row pitch 2 BK = 64 or 128 bytes): f(r) = (r / rows-per-256-bytes) & (chunks - 1);
+//      B, 32x32 layout (row pitch 2 BN >= 128 bytes): f(k) = 4 ((k / rows-per-256-bytes) & (QB - 1)),
+//        so the 4 rows x 64 bytes of a ds_read_b64_tr_b16 half-wave land on distinct bank groups;
+//      B, 16x16 layout (row pitch >= 256 bytes): 32-byte chunks XORed with
+//        h(k) = (k & 3) | ((k >> 3) & 1) << 2, so the 8 rows x 32 bytes of a half-wave do.
+//    Measured with the LDS bank-conflict counters: every combination in use is conflict-free except
+//    A with 64-byte rows in the 16x16 layout (BK = 32), which conflicts on a sixth of its cycles; the
+//    16x16 tiles that matter use BK = 64.
+//  * The MFMA B operand (A^T columns, 8 consecutive k per lane) is one ds_read_b128 per lane; the
+//    MFMA A operand (B^T rows) comes from two transposing reads ds_read_b64_tr_b16 of B kept as
+//    [k][n]: in each 16-lane group, lane L addresses row k0 + (L >> 2) at columns n0 + 4 (L & 3),
+//    and result lane i then holds B[k0 + e][n0 + i] for e = 0..3. No register shuffles.
+//  * Two schedules (SCHED). 0: one fragment buffer per chunk, the compiler interleaving the next
+//    chunk's reads with the current MFMAs (scheduling-group hints). 1: fragments double-buffered in
+//    registers across chunks and slabs; in a slab's last chunk the barrier comes first, then the
+//    refill of the slot just freed is spread one LDS-DMA instruction per group of MFMAs (a burst of
+//    DMA issue would leave the MFMA pipe idle with one or two waves per SIMD) together with the next
+//    slab's first reads. The DMA is branch-free (past the last slab it reads zeros), so every slab
+//    takes the same step and no tail code keeps fragments live into the epilogue.
 //  * Each XCD (own L2) walks one rectangle of the tile grid in GROUP_M-grouped order (the split with
 //    the smallest A + B panel footprint, chosen by the host), or, when the grid does not split into
 //    8 equal rectangles, a contiguous range of the flat grouped order.
@@ -44,12 +55,61 @@ __device__ inline u32x2 gemm_lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool SHALLOW = false>
+template <int MI>
+struct GemmAcc {
+  typedef floatx16 type;  // v_mfma_f32_32x32x16_f16: 16 accumulators per lane
+};
+template <>
+struct GemmAcc<16> {
+  typedef floatx4 type;  // v_mfma_f32_16x16x32_f16: 4 accumulators per lane
+};
+
+// MI: MFMA shape (32: v_mfma_f32_32x32x16_f16, 16: v_mfma_f32_16x16x32_f16). SCHED: 0 = one fragment
+// buffer per chunk, scheduled by the compiler; 1 = fragments double-buffered across chunks and
+// slabs, LDS-DMA spread over the last chunk's MFMAs.
+template <int BM, int BN, int BK, int WM, int WN, bool SHALLOW, int MI, int SCHED>
 struct GemmKernel {
   static constexpr int WAVES = WM * WN;
-  static constexpr int TM = BM / WM / 32;  // 32-row tiles per wave along M
-  static constexpr int TN = BN / WN / 32;  // 32-col tiles per wave along N
-  static constexpr int KCH = BK / 16;      // 16-deep MFMA chunks per slab
+  static constexpr int KD = MI == 32 ? 16 : 32;  // k depth of one MFMA
+  static constexpr int TM = BM / WM / MI;        // MI-row tiles per wave along M
+  static constexpr int TN = BN / WN / MI;        // MI-col tiles per wave along N
+  static constexpr int KCH = BK / KD;            // MFMA-deep chunks per slab
+  typedef typename GemmAcc<MI>::type Acc;
+  // Accumulators of the wave's TN x TM MFMA tiles. 16x16 tiles are stored four to a floatx16 (tile
+  // tm in elements 4 (tm % 4) .. 4 (tm % 4) + 3 of vector tm / 4), so the register allocator works
+  // with 16-register tuples as for the 32x32 tiles.
+  static constexpr int AG = (MI == 16 && TM % 4 == 0) ? 4 : 1;
+  struct AccTiles {
+    floatx16 v[TN][AG == 4 ? TM / 4 : (MI == 32 ? TM : 1)];
+    Acc t[TN][AG == 4 || MI == 32 ? 1 : TM];
+  };
+  __device__ __attribute__((always_inline)) static inline void mma(AccTiles& acc, int tn, int tm, const u32x4& b,
+                                                                   const u32x4& a) {
+    if constexpr (MI == 32) {
+      acc.v[tn][tm] = DT<f16_t>::mfma32(b, a, acc.v[tn][tm]);
+    } else if constexpr (AG == 4) {
+      floatx16& g = acc.v[tn][tm / 4];
+      const int q = 4 * (tm % 4);
+      floatx4 c = {g[q], g[q + 1], g[q + 2], g[q + 3]};
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b), __builtin_bit_cast(half8, a), c, 0, 0, 0);
+      g[q] = c[0];
+      g[q + 1] = c[1];
+      g[q + 2] = c[2];
+      g[q + 3] = c[3];
+    } else {
+      acc.t[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, b), __builtin_bit_cast(half8, a),
+                                                             acc.t[tn][tm], 0, 0, 0);
+    }
+  }
+  __device__ __attribute__((always_inline)) static inline float acc_at(const AccTiles& acc, int tn, int tm, int r) {
+    if constexpr (MI == 32)
+      return acc.v[tn][tm][r];
+    else if constexpr (AG == 4)
+      return acc.v[tn][tm / 4][4 * (tm % 4) + r];
+    else
+      return acc.t[tn][tm][r];
+  }
+  static constexpr int ACC = MI == 32 ? 16 : 4;
   static constexpr int AP = BK * 2;        // A row pitch in LDS (bytes)
   static constexpr int BP = BN * 2;        // B row pitch in LDS (bytes)
   static constexpr int SA = BK / 8;        // 16-byte chunks per A row
@@ -71,7 +131,11 @@ struct GemmKernel {
   static constexpr int B_PER_WAVE = B_BYTES / 1024 / WAVES;
   static constexpr int DMA_PER_SLAB = A_PER_WAVE + B_PER_WAVE;
   static constexpr int READS = TM + 2 * TN;  // LDS reads per chunk
-  static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile shape");
+  static constexpr bool kPipe = SCHED == 1;
+  static_assert(MI == 32 || MI == 16, "MFMA shape");
+  static_assert(SCHED == 0 || SCHED == 1, "schedule");
+  static_assert(TM >= 1 && TN >= 1 && BK % KD == 0, "tile shape");
+  static_assert(MI == 32 || BP >= 256, "16x16 B swizzle assumes rows of at least 256 bytes");
   static_assert(AP == 64 || AP == 128, "A swizzle assumes 64- or 128-byte rows");
   static_assert(BP >= 128 && QB >= 2, "B swizzle assumes rows of at least 128 bytes");
   static_assert(A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0, "slab must split evenly");
@@ -80,38 +144,155 @@ struct GemmKernel {
   static constexpr int CHS = CP / 16 < 16 ? CP / 16 : 16;  // swizzled 16-byte chunks per C row
   static_assert(BM * CP <= RING * SLAB_BYTES, "the C tile is staged in the slab ring");
 
-  __device__ static inline void compute(floatx16 (&acc)[TN][TM], const char* slab, const uint32_t (&aaddr)[KCH],
-                                        const uint32_t (&baddr)[TN], int wm) {
+  // Fragments of one KD-deep chunk: TM A^T column blocks (ds_read_b128) and TN B^T row blocks (two
+  // transposing reads each).
+  struct Frag {
+    u32x4 a[TM];
+    u32x4 b[TN];
+  };
+
+  template <int C>
+  __device__ __attribute__((always_inline)) static inline void read_frag(Frag& f, const char* slab, const uint32_t (&aaddr)[KCH],
+                                          const uint32_t (&baddr)[TN], int wm) {
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      u32x4 af[TM], bf[TN];
+    for (int tm = 0; tm < TM; ++tm)
+      f.a[tm] = *reinterpret_cast<const u32x4*>(slab + aaddr[C] + (wm * TM + tm) * MI * AP);
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-        af[tm] = *reinterpret_cast<const u32x4*>(slab + aaddr[c] + (wm * TM + tm) * 32 * AP);
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const char* base = slab + A_BYTES + baddr[tn] + c * 16 * BP;
-        const u32x2 lo = gemm_lds_read_tr16(base);
-        const u32x2 hi = gemm_lds_read_tr16(base + 4 * BP);
-        bf[tn] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-      }
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = DT<f16_t>::mfma32(bf[tn], af[tm], acc[tn][tm]);
+    for (int tn = 0; tn < TN; ++tn) {
+      const char* base = slab + A_BYTES + baddr[tn] + C * KD * BP;
+      const u32x2 lo = gemm_lds_read_tr16(base);
+      const u32x2 hi = gemm_lds_read_tr16(base + 4 * BP);
+      f.b[tn] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
     }
-    // The reads of chunk c+1 are issued while chunk c's MFMAs run.
-    __builtin_amdgcn_sched_group_barrier(0x100, READS, 0);
+  }
+
+  __device__ __attribute__((always_inline)) static inline void mfma_frag(AccTiles& acc, const Frag& f) {
 #pragma unroll
-    for (int i = 0; i < KCH * TM * TN; ++i) {
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) mma(acc, tn, tm, f.b[tn], f.a[tm]);
+  }
+
+
+
+  // Read R of a chunk's fragments (0..TM-1: A blocks; then B block (R - TM) / 2, low or high half).
+  template <int C, int R>
+  __device__ __attribute__((always_inline)) static inline void read_one(Frag& f, const char* slab, const uint32_t (&aaddr)[KCH],
+                                         const uint32_t (&baddr)[TN], int wm) {
+    if constexpr (R < TM) {
+      f.a[R] = *reinterpret_cast<const u32x4*>(slab + aaddr[C] + (wm * TM + R) * MI * AP);
+    } else {
+      constexpr int tn = (R - TM) / 2, hi = (R - TM) & 1;
+      const u32x2 v = gemm_lds_read_tr16(slab + A_BYTES + baddr[tn] + C * KD * BP + hi * 4 * BP);
+      f.b[tn][2 * hi] = v[0];
+      f.b[tn][2 * hi + 1] = v[1];
+    }
+  }
+
+  template <int C, int R0, int R1>
+  __device__ __attribute__((always_inline)) static inline void read_range(Frag& f, const char* slab, const uint32_t (&aaddr)[KCH],
+                                           const uint32_t (&baddr)[TN], int wm) {
+    if constexpr (R0 < R1) {
+      read_one<C, R0>(f, slab, aaddr, baddr, wm);
+      read_range<C, R0 + 1, R1>(f, slab, aaddr, baddr, wm);
+    }
+  }
+
+  // MFMAs M0..M1-1 of a chunk (MFMA m: B block m / TM, A block m % TM).
+  template <int M0, int M1>
+  __device__ __attribute__((always_inline)) static inline void mfma_range(AccTiles& acc, const Frag& f) {
+    if constexpr (M0 < M1) {
+      mma(acc, M0 / TM, M0 % TM, f.b[M0 / TM], f.a[M0 % TM]);
+      mfma_range<M0 + 1, M1>(acc, f);
+    }
+  }
+
+
+  // NM MFMAs, each followed by its share of NR LDS reads.
+  template <int NM, int NR, int I = 0, int LEFT = NR>
+  __device__ __attribute__((always_inline)) static inline void interleave_n() {
+    constexpr int kPer = NM > 0 ? (NR + NM - 1) / NM : 0;
+    if constexpr (I < NM) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, (READS + TM * TN - 1) / (TM * TN), 0);
+      constexpr int kReads = LEFT < kPer ? LEFT : kPer;
+      if constexpr (kReads > 0) __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
+      interleave_n<NM, NR, I + 1, LEFT - kReads>();
+    }
+  }
+
+  // The last chunk of a slab with a successor, in DMA_PER_SLAB groups: group G issues LDS-DMA
+  // instruction G of slab ks + RING (into the slot every wave finished at the barrier), its share of
+  // the next slab's first-chunk reads and its share of this chunk's MFMAs, so the DMA issue is
+  // spread over the MFMA stream instead of stalling it in one burst.
+  template <int G, class Dma>
+  __device__ __attribute__((always_inline)) static inline void last_chunk_groups(
+      AccTiles& acc, const Frag& cur, Frag& nxt, const char* next, const uint32_t (&aaddr)[KCH],
+      const uint32_t (&baddr)[TN], int wm, Dma& dma) {
+    constexpr int NG = DMA_PER_SLAB, MF = TM * TN;
+    if constexpr (G < NG) {
+      constexpr int R0 = G * READS / NG, R1 = (G + 1) * READS / NG;
+      constexpr int M0 = G * MF / NG, M1 = (G + 1) * MF / NG;
+      dma(std::integral_constant<int, G>{});
+      read_range<0, R0, R1>(nxt, next, aaddr, baddr, wm);
+      mfma_range<M0, M1>(acc, cur);
+      interleave_n<M1 - M0, R1 - R0>();
+      __builtin_amdgcn_sched_barrier(0);
+      last_chunk_groups<G + 1>(acc, cur, nxt, next, aaddr, baddr, wm, dma);
+    }
+  }
+
+  // Chunks C.. of a slab with one fragment buffer per chunk (the compiler allocates and schedules
+  // them): the reads of chunk c+1 are issued while chunk c's MFMAs run.
+  template <int C = 0>
+  __device__ static inline void compute(AccTiles& acc, const char* slab, const uint32_t (&aaddr)[KCH],
+                                        const uint32_t (&baddr)[TN], int wm) {
+    if constexpr (C < KCH) {
+      Frag f;
+      read_frag<C>(f, slab, aaddr, baddr, wm);
+      mfma_frag(acc, f);
+      compute<C + 1>(acc, slab, aaddr, baddr, wm);
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x100, READS, 0);
+#pragma unroll
+      for (int i = 0; i < KCH * TM * TN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (READS + TM * TN - 1) / (TM * TN), 0);
+      }
+    }
+  }
+
+  // Chunk C of a slab in the double-buffered loop; the slab's chunk 0 uses fragment buffer BUF0
+  // and chunk C buffer (BUF0 + C) & 1. Before a slab's last chunk `wait` synchronises the workgroup
+  // and returns the next slab, `dma(J)` issues LDS-DMA instruction J of the slab that refills the
+  // ring, and the next slab's first chunk is read into the buffer that follows.
+  template <int BUF0, int C, class Wait, class Dma>
+  __device__ __attribute__((always_inline)) static inline void chunk_step(
+      AccTiles& acc, Frag (&f)[2], const char* slab, const uint32_t (&aaddr)[KCH], const uint32_t (&baddr)[TN],
+      int wm, Wait& wait, Dma& dma) {
+    constexpr int kCur = (BUF0 + C) & 1, kNext = (BUF0 + C + 1) & 1;
+    if constexpr (C + 1 < KCH) {
+      read_frag<C + 1>(f[kNext], slab, aaddr, baddr, wm);
+      mfma_frag(acc, f[kCur]);
+      interleave_n<TM * TN, READS>();
+      __builtin_amdgcn_sched_barrier(0);
+      chunk_step<BUF0, C + 1>(acc, f, slab, aaddr, baddr, wm, wait, dma);
+    } else {
+      const char* next = wait();
+      last_chunk_groups<0>(acc, f[kCur], f[kNext], next, aaddr, baddr, wm, dma);
+    }
+  }
+
+  template <int J, class Dma>
+  __device__ __attribute__((always_inline)) static inline void dma_all(Dma& dma) {
+    if constexpr (J < DMA_PER_SLAB) {
+      dma(std::integral_constant<int, J>{});
+      dma_all<J + 1>(dma);
     }
   }
 
   __device__ static void run(const GemmParams& p) {
     __shared__ __attribute__((aligned(16))) char smem[RING * SLAB_BYTES];
-    const int tid = threadIdx.x;
+    const int tid = (int)__builtin_amdgcn_workitem_id_x();
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hh = lane >> 5;
     const int wm = wave / WN, wn = wave % WN;
@@ -124,7 +305,7 @@ struct GemmKernel {
       // every B panel.
       constexpr int kXcds = 8;
       const int rn = kXcds / p.region_m;
-      const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+      const int xcd = (int)__builtin_amdgcn_workgroup_id_x() % kXcds, slot = (int)__builtin_amdgcn_workgroup_id_x() / kXcds;
       const int rt_m = p.tiles_m / p.region_m, rt_n = p.tiles_n / rn;
       const int in_group = p.group_m * rt_n;
       const int first_m = (slot / in_group) * p.group_m;
@@ -133,7 +314,7 @@ struct GemmKernel {
       pid_n = (xcd % rn) * rt_n + (slot % in_group) / gsz;
     } else {
       const int total = p.tiles_m * p.tiles_n;
-      const int pid = xcd_remap(blockIdx.x, total);
+      const int pid = xcd_remap((int)__builtin_amdgcn_workgroup_id_x(), total);
       const int in_group = p.group_m * p.tiles_n;
       const int first_m = (pid / in_group) * p.group_m;
       const int gsz = min(p.tiles_m - first_m, p.group_m);
@@ -165,7 +346,7 @@ struct GemmKernel {
     for (int j = 0; j < B_PER_WAVE; ++j) {
       const int byte = (wave * B_PER_WAVE + j) * 1024 + lane * 16;
       const int k = byte / BP, s = (byte % BP) / 16;
-      const int c = s ^ (4 * ((k / RB) & (QB - 1)));
+      const int c = MI == 32 ? s ^ (4 * ((k / RB) & (QB - 1))) : s ^ (2 * ((k & 3) | (((k >> 3) & 1) << 2)));
       boffs[j] = ((uint32_t)k * (uint32_t)p.ldb + c * 8) * 2u;
     }
 
@@ -176,7 +357,25 @@ struct GemmKernel {
     // neither of which changes k's swizzle term w) at logical chunk 4 jt + sb, byte 8 (L & 1) of it;
     // slot = 4 (jt ^ w) + sb.
     uint32_t aaddr[KCH], baddr[TN];
-    {
+    if constexpr (MI == 16) {
+      // A: lane reads row r16 = lane & 15 of each 16-row tile at logical chunk 4c + g (g = lane >> 4),
+      // slot (4c + g) ^ x = 4c ^ (g ^ x), x = (r16 / RA) & (SA - 1): address (r16*AP + 16 (g ^ x)) ^ 64 c.
+      // B: lane reads row k = 8 g + (r16 >> 2) (+32 per chunk, +4 for the second read) at byte
+      // 8 (r16 & 3) of logical 32-byte chunk jt (16-column tile), stored at 32-byte slot jt ^ h with
+      // h = (k & 3) | ((k >> 3) & 1) << 2 = (r16 >> 2) | (g & 1) << 2: the 8 rows one half-wave reads
+      // land on the 8 distinct 32-byte bank groups of a 256-byte line.
+      const int r16 = lane & 15, g = lane >> 4;
+      const int x = (r16 / RA) & (SA - 1);
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) aaddr[c] = (uint32_t)((r16 * AP + 16 * (g ^ x)) ^ (64 * c));
+      const int kr = 8 * g + (r16 >> 2);
+      const int h = (r16 >> 2) | ((g & 1) << 2);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int jt = wn * TN + tn;
+        baddr[tn] = (uint32_t)(kr * BP + 32 * (jt ^ h) + 8 * (r16 & 3));
+      }
+    } else {
       const int x = (col / RA) & (SA - 1);
 #pragma unroll
       for (int c = 0; c < KCH; ++c) aaddr[c] = (uint32_t)((col * AP + 16 * (hh ^ x)) ^ (32 * c));
@@ -196,44 +395,113 @@ struct GemmKernel {
     const bool k_ragged = (p.K % BK) != 0;  // last slab runs past K: A chunks there read zeros
     const uint32_t smem_lds = lds_address(smem);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // scalar DMA destinations
-    auto issue = [&](int ks) {
+    // DMA instruction j (A blocks first, then B blocks) of slab ks; nothing past the last slab.
+    auto issue_one = [&](int ks, int j) {
       if (ks >= ksteps) return;
       const uint32_t slot = smem_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
-      const bool tail = k_ragged && ks == ksteps - 1;
-#pragma unroll
-      for (int j = 0; j < A_PER_WAVE; ++j) {
+      if (j < A_PER_WAVE) {
         // past-K chunks of the ragged slab get an offset beyond the range (zeros): A's rows may hold
         // anything there, and 0 * NaN would reach valid outputs. 2^31 is past every range (the host
         // keeps spans below 2 GiB) and far from 32-bit wrap-around.
+        const bool tail = k_ragged && ks == ksteps - 1;
         const uint32_t off = (tail && ks * BK + ak0[j] >= p.K) ? 0x80000000u : aoffs[j] + (uint32_t)ks * a_slab_bytes;
         buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
+      } else {
+        const int jb = j - A_PER_WAVE;
+        buffer_load16_to_lds(brs, boffs[jb] + (uint32_t)ks * b_slab_bytes,
+                             slot + A_BYTES + (wave_u * B_PER_WAVE + jb) * 1024);
       }
+    };
+    auto issue = [&](int ks) {
 #pragma unroll
-      for (int j = 0; j < B_PER_WAVE; ++j)
-        buffer_load16_to_lds(brs, boffs[j] + (uint32_t)ks * b_slab_bytes,
-                             slot + A_BYTES + (wave_u * B_PER_WAVE + j) * 1024);
+      for (int j = 0; j < DMA_PER_SLAB; ++j) issue_one(ks, j);
     };
 
-    floatx16 acc[TN][TM];
+    AccTiles acc;
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn)
+    for (int tn = 0; tn < TN; ++tn) {
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
+      for (int i = 0; i < (int)(sizeof(acc.v[0]) / sizeof(floatx16)); ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[tn][tm][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc.v[tn][i][r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < (int)(sizeof(acc.t[0]) / sizeof(Acc)); ++i)
+#pragma unroll
+        for (int r = 0; r < ACC; ++r) acc.t[tn][i][r] = 0.f;
+    }
 
+    if constexpr (kPipe) {
+      // Fragments double-buffered in registers across chunks and slabs: chunk c's MFMAs run while
+      // chunk c+1's fragments are read; in a slab's last chunk the barrier comes first (slab ks+1
+      // landed, every wave done reading slab ks), then the DMA into slab ks's slot and the reads of
+      // slab ks+1's first chunk, interleaved with the last chunk's MFMAs.
+      // DMA instruction J of slab ks, branch-free: past the last slab it reads an offset beyond the
+      // range, so the slot holds zeros, and exactly RING - 2 slabs are always in flight behind the
+      // one a barrier waits for.
+      auto dma_slab = [&](int ks, auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        const uint32_t slot = smem_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
+        const bool live = ks < ksteps;
+        if constexpr (j < A_PER_WAVE) {
+          // bitwise, not short-circuit: the scalar and per-lane parts stay one select
+          const bool zero = !live | (k_ragged & (ks == ksteps - 1) & (ks * BK + ak0[j] >= p.K));
+          const uint32_t off = zero ? 0x80000000u : aoffs[j] + (uint32_t)ks * a_slab_bytes;
+          buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
+        } else {
+          constexpr int jb = j - A_PER_WAVE;
+          const uint32_t off = live ? boffs[jb] + (uint32_t)ks * b_slab_bytes : 0x80000000u;
+          buffer_load16_to_lds(brs, off, slot + A_BYTES + (wave_u * B_PER_WAVE + jb) * 1024);
+        }
+      };
+      // Prologue: slabs 0 .. RING-1 (zeros past the last one: the loop below may multiply one slab
+      // past it); slab 0 must have landed in every wave's part before its first reads.
 #pragma unroll
-    for (int s = 0; s + 1 < RING; ++s) issue(s);
-    wait_vm_lds_barrier<0>();
-
-    for (int ks = 0; ks < ksteps; ++ks) {
-      issue(ks + RING - 1);  // into the slot slab ks-1 left (read in step ks-1)
-      compute(acc, smem + (ks % RING) * SLAB_BYTES, aaddr, baddr, wm);
-      // Step ks+1 reads slab ks+1; the RING-2 newer slabs may stay in flight.
-      if (RING > 2 && ks + RING - 1 < ksteps)
-        wait_vm_lds_barrier<(RING > 2 ? (RING - 2) * DMA_PER_SLAB : 0)>();
-      else
-        wait_vm_lds_barrier<0>();
+      for (int s0 = 0; s0 < RING; ++s0) {
+        auto d = [&](auto jc) __attribute__((always_inline)) { dma_slab(s0, jc); };
+        dma_all<0>(d);
+      }
+      wait_vm_lds_barrier<(RING - 1) * DMA_PER_SLAB>();
+      Frag f[2];
+      read_frag<0>(f[0], smem, aaddr, baddr, wm);
+      // Every slab takes the same step (barrier, refill, next slab's first reads): the last one
+      // reads a slab that is never multiplied. Slab ks's chunk 0 uses buffer (ks * KCH) & 1, so with an
+      // odd chunk count slabs go in pairs and an odd slab count gets one more slab, which the
+      // branch-free DMA fills with zeros (its products add exactly 0). No tail code: the epilogue
+      // starts with only the accumulators live.
+      auto slab_step = [&](int ks, auto par_c) __attribute__((always_inline)) {
+        const char* slab = smem + (ks % RING) * SLAB_BYTES;
+        // Slab ks+1 must have landed; the RING - 2 slabs after it stay in flight.
+        auto wait = [&]() __attribute__((always_inline)) {
+          wait_vm_lds_barrier<(RING - 2) * DMA_PER_SLAB>();
+          __builtin_amdgcn_sched_barrier(0);
+          return smem + ((ks + 1) % RING) * SLAB_BYTES;
+        };
+        // Slab ks + RING goes into slab ks's slot: every wave passed the barrier.
+        auto dma = [&](auto jc) __attribute__((always_inline)) { dma_slab(ks + RING, jc); };
+        chunk_step<(decltype(par_c)::value * KCH) & 1, 0>(acc, f, slab, aaddr, baddr, wm, wait, dma);
+      };
+      if constexpr (KCH % 2 == 0) {
+        for (int ks = 0; ks < ksteps; ++ks) slab_step(ks, std::integral_constant<int, 0>{});
+      } else {
+        for (int ks = 0; ks < ksteps; ks += 2) {
+          slab_step(ks, std::integral_constant<int, 0>{});
+          slab_step(ks + 1, std::integral_constant<int, 1>{});
+        }
+      }
+      wait_vm_lds_barrier<0>();  // every wave done with the ring before it holds the C tile
+    } else {
+#pragma unroll
+      for (int s0 = 0; s0 + 1 < RING; ++s0) issue(s0);
+      wait_vm_lds_barrier<0>();
+      for (int ks = 0; ks < ksteps; ++ks) {
+        issue(ks + RING - 1);  // into the slot slab ks-1 left (read in step ks-1)
+        compute(acc, smem + (ks % RING) * SLAB_BYTES, aaddr, baddr, wm);
+        // Step ks+1 reads slab ks+1; the RING-2 newer slabs may stay in flight.
+        if (RING > 2 && ks + RING - 1 < ksteps)
+          wait_vm_lds_barrier<(RING > 2 ? (RING - 2) * DMA_PER_SLAB : 0)>();
+        else
+          wait_vm_lds_barrier<0>();
+      }
     }
 
     // C goes out through LDS (the ring is free after the last step's barrier): each lane holds 4
@@ -244,16 +512,19 @@ struct GemmKernel {
     char* ctile = smem;
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      const int r = (wm * TM + tm) * 32 + col;
+      // 32x32: lane holds row col, columns 8 gq + 4 hh + 0..3; 16x16: row lane & 15, columns
+      // 4 (lane >> 4) + 0..3.
+      const int r = (wm * TM + tm) * MI + (MI == 32 ? col : (lane & 15));
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int cb = ((wn * TN + tn) * 32 + 8 * gq + 4 * hh) * 2;  // byte column in the tile row
+        for (int gq = 0; gq < ACC / 4; ++gq) {
+          const int cb = MI == 32 ? ((wn * TN + tn) * 32 + 8 * gq + 4 * hh) * 2   // byte column in the tile row
+                                  : ((wn * TN + tn) * 16 + 4 * (lane >> 4)) * 2;
           const int phys = r * CP + ((((cb >> 4) ^ (r & (CHS - 1)))) << 4) + (cb & 15);
           *reinterpret_cast<u32x2*>(ctile + phys) =
-              (u32x2){DT<f16_t>::pack2(acc[tn][tm][4 * gq], acc[tn][tm][4 * gq + 1]),
-                      DT<f16_t>::pack2(acc[tn][tm][4 * gq + 2], acc[tn][tm][4 * gq + 3])};
+              (u32x2){DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq), acc_at(acc, tn, tm, 4 * gq + 1)),
+                      DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq + 2), acc_at(acc, tn, tm, 4 * gq + 3))};
         }
     }
     __syncthreads();
@@ -279,40 +550,45 @@ struct GemmKernel {
   }
 };
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(GemmParams p) {
-  GemmKernel<BM, BN, BK, WM, WN>::run(p);
+  GemmKernel<BM, BN, BK, WM, WN, false, MI, SCHED>::run(p);
 }
 
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_shallow_kernel(GemmParams p) {
-  GemmKernel<BM, BN, BK, WM, WN, true>::run(p);
+  GemmKernel<BM, BN, BK, WM, WN, true, MI, SCHED>::run(p);
 }
 
 // The shallow-ring kernel of a tile, or nullptr when its ring would be as deep as the default one.
-template <int BM, int BN, int BK, int WM, int WN>
+template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
 const void* gemm_shallow_fn() {
-  if constexpr (GemmKernel<BM, BN, BK, WM, WN, true>::RING < GemmKernel<BM, BN, BK, WM, WN>::RING)
-    return (const void*)&gemm_f16_shallow_kernel<BM, BN, BK, WM, WN>;
+  if constexpr (GemmKernel<BM, BN, BK, WM, WN, true, MI, SCHED>::RING < GemmKernel<BM, BN, BK, WM, WN, false, MI, SCHED>::RING)
+    return (const void*)&gemm_f16_shallow_kernel<BM, BN, BK, WM, WN, MI, SCHED>;
   else
     return nullptr;
 }
 
-#define GEMM_ENTRY(BM, BN, BK, WM, WN)                                                  \
-  {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN>,             \
-   gemm_shallow_fn<BM, BN, BK, WM, WN>(),                                               \
-   "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "EEEvNS_10GemmParamsE"}
+#define GEMM_ENTRY(BM, BN, BK, WM, WN, MI, SCHED)                                                         \
+  {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN, MI, SCHED>,                    \
+   gemm_shallow_fn<BM, BN, BK, WM, WN, MI, SCHED>(),                                                      \
+   "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "ELi" #MI "ELi" #SCHED \
+   "EEEvNS_10GemmParamsE"}
 
+// One kernel per tile: the MFMA shape and schedule measured fastest for it on MI355X (16x16x32
+// MFMAs draw less power per flop, which raises the clock of the 8-wave tiles; the pipelined
+// schedule pays where one or two waves per SIMD would otherwise wait on LDS and barriers).
 static const GemmKernelEntry kGemmEntries[] = {
-    GEMM_ENTRY(256, 256, 64, 2, 4),
-    GEMM_ENTRY(256, 256, 32, 2, 4),
-    GEMM_ENTRY(256, 128, 64, 2, 4),
-    GEMM_ENTRY(128, 256, 64, 2, 4),
-    GEMM_ENTRY(256, 256, 64, 2, 2),
-    GEMM_ENTRY(128, 128, 64, 2, 2),
-    GEMM_ENTRY(128, 128, 32, 2, 2),
-    GEMM_ENTRY(128, 64, 32, 2, 2),
-    GEMM_ENTRY(64, 256, 32, 2, 2),
+    GEMM_ENTRY(256, 256, 64, 2, 4, 16, 1),
+    GEMM_ENTRY(256, 256, 32, 2, 4, 16, 1),
+    GEMM_ENTRY(256, 128, 64, 2, 4, 16, 1),
+    GEMM_ENTRY(128, 256, 64, 2, 4, 16, 1),
+    GEMM_ENTRY(256, 256, 64, 2, 2, 32, 1),
+    GEMM_ENTRY(256, 256, 32, 2, 2, 32, 1),
+    GEMM_ENTRY(128, 128, 64, 2, 2, 32, 1),
+    GEMM_ENTRY(128, 128, 32, 2, 2, 32, 1),
+    GEMM_ENTRY(128, 64, 32, 2, 2, 32, 0),
+    GEMM_ENTRY(64, 256, 32, 2, 2, 16, 1),
 };
 
 const GemmKernelEntry* gemm_registry(int* count) {

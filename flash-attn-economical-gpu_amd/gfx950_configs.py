@@ -76,6 +76,7 @@ GEMM_TILE_SPACE = [
     (256, 256, 64, 8),
     (256, 256, 64, 4),
     (256, 256, 32, 8),
+    (256, 256, 32, 4),
     (256, 128, 64, 8),
     (128, 256, 64, 8),
     (128, 128, 64, 4),

@@ -66,6 +66,24 @@ def _time(fn, warmup: int, iters: int, batch_ms: float = 1.0) -> float:
     return statistics.median(sample(batch) for _ in range(iters))
 
 
+REFINE_TOP = 3
+REFINE_ROUNDS = 5
+
+
+def _refine(fns: dict, results: dict, top: int = REFINE_TOP, rounds: int = REFINE_ROUNDS, iters: int = 3) -> dict:
+    """Re-time the `top` fastest candidates of a first pass in `rounds` interleaved rounds and
+    return their medians: tiles within a few percent of each other are then ranked under the same
+    clock and thermal conditions rather than by one pass each, minutes apart."""
+    best = sorted(results, key=results.get)[:top]
+    if len(best) < 2:
+        return {}
+    samples: dict = {k: [] for k in best}
+    for _ in range(rounds):
+        for k in best:
+            samples[k].append(_time(fns[k], 1, iters))
+    return {k: round(statistics.median(v), 4) for k, v in samples.items()}
+
+
 def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5, log=print) -> None:
     dev = torch.device("cuda:0")
     for name, dtype, B, H, Hkv, M, N, D, causal, variants in sweep:
@@ -76,7 +94,7 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
         flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal and M == N else M * N)
         for vname in variants:
             variant = VARIANTS[vname]
-            results = {}
+            results, fns = {}, {}
             for cand in cfgs.fa_candidates(variant, dtype, D):
                 splits = 1
                 ws = None
@@ -88,10 +106,13 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
                     need = hip_lib.workspace_bytes(B, H, M, D, splits)
                     ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
                 tile = cfgs.FaTileChoice(cand.block_m, cand.block_n, cand.waves, cand.stages, splits).to_c()
-                ms = _time(lambda: hip_lib.fa_fwd(q, k, v, o, None, sm_scale=D ** -0.5, causal=causal,
-                                                  variant=variant, tile=tile, workspace=ws), warmup, iters)
-                results[f"{cand.block_m}x{cand.block_n}x{cand.waves}x{cand.stages}"] = round(ms, 4)
-            best = min(results, key=results.get)
+                key = f"{cand.block_m}x{cand.block_n}x{cand.waves}x{cand.stages}"
+                fns[key] = (lambda tile=tile, ws=ws, variant=variant: hip_lib.fa_fwd(
+                    q, k, v, o, None, sm_scale=D ** -0.5, causal=causal, variant=variant, tile=tile, workspace=ws))
+                results[key] = round(_time(fns[key], warmup, iters), 4)
+            refined = _refine(fns, results)
+            results.update(refined)
+            best = min(refined or results, key=(refined or results).get)
             key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, M, N)
             table["fa"][key] = {
                 "tile": [int(x) for x in best.split("x")],
@@ -111,17 +132,20 @@ def tune_gemm(table: dict, sweep=GEMM_SWEEP, warmup: int = 2, iters: int = 5, lo
         a = (torch.rand(M, K, device=dev) * 2 - 1).half()
         b = (torch.rand(K, N, device=dev) * 2 - 1).half()
         c = torch.empty(M, N, device=dev, dtype=torch.float16)
-        results = {}
+        results, fns = {}, {}
         for t in cfgs.gemm_candidates():
             if M % t[0] or N % t[1] or K % t[2]:
                 continue
             for gm in GROUP_MS:
                 gt = hip_lib.GemmTile(t[0], t[1], t[2], t[3], gm)
-                results[f"{t[0]}x{t[1]}x{t[2]}x{t[3]}g{gm}"] = round(
-                    _time(lambda: hip_lib.gemm_f16(a, b, c, gt), warmup, iters), 4)
+                key = f"{t[0]}x{t[1]}x{t[2]}x{t[3]}g{gm}"
+                fns[key] = lambda gt=gt: hip_lib.gemm_f16(a, b, c, gt)
+                results[key] = round(_time(fns[key], warmup, iters), 4)
         if not results:
             continue
-        best = min(results, key=results.get)
+        refined = _refine(fns, results)
+        results.update(refined)
+        best = min(refined or results, key=(refined or results).get)
         tile_part, gm_part = best.split("g")
         table["gemm"][cfgs.gemm_table_key(M, N, K)] = {
             "tile": [int(x) for x in tile_part.split("x")],

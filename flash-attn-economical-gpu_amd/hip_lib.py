@@ -18,7 +18,7 @@ import torch
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libfa_gfx950.so"
 RESOURCES_PATH = HERE / "kernel_resources.json"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 FA_OK, FA_EINVAL, FA_ENOTSUP, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
 FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1
@@ -128,6 +128,13 @@ SIGNATURES = {
         [
             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
             ctypes.POINTER(FaTile), ctypes.POINTER(GemmTile), ctypes.POINTER(FaResources),
+        ],
+    ),
+    "fa_kernel_symbol": (
+        ctypes.c_int,
+        [
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+            ctypes.POINTER(FaTile), ctypes.POINTER(GemmTile), ctypes.c_char_p, ctypes.c_int32,
         ],
     ),
     "fa_device_limits": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(FaDeviceLimits)]),
@@ -368,23 +375,25 @@ def compiled_resources() -> dict[str, dict[str, object]]:
     return _resource_table
 
 
-def fwd_kernel_symbol(variant: int, dtype: torch.dtype, D: int, tile: FaTile) -> str:
-    """Mangled name of the attention instantiation a tile resolves to (as in kernel_resources.json)."""
-    tag = {torch.float16: "5f16_t", torch.bfloat16: "6bf16_t"}[dtype]
-    # the pipeline the C ABI resolves (stages_of in csrc/fa_abi.hip)
-    stages = 1 if variant == FA_VARIANT_BASIC else (tile.stages if tile.stages in (3, 4, 5) else 2)
-    rows = tile.block_m // tile.waves
-    rt = rows // 32
-    split = "1" if (variant == FA_VARIANT_SLICED and tile.splits > 1) else "0"
-    return (
-        f"_ZN2fa13fa_fwd_kernelINS_{tag}ELi{D}ELi{tile.waves}ELi{rt}ELi{tile.block_n}"
-        f"ELi{stages}ELb{split}EEEvNS_9FwdParamsE"
+def _kernel_symbol(op: int, variant: int, dtype: torch.dtype, D: int, tile: FaTile | None,
+                   gtile: GemmTile | None) -> str:
+    buf = ctypes.create_string_buffer(512)
+    code = load().fa_kernel_symbol(
+        op, variant, dtype_code(dtype), D,
+        ctypes.byref(tile) if tile is not None else None,
+        ctypes.byref(gtile) if gtile is not None else None,
+        buf, len(buf),
     )
+    check(code, "fa_kernel_symbol")
+    return buf.value.decode()
+
+
+def fwd_kernel_symbol(variant: int, dtype: torch.dtype, D: int, tile: FaTile) -> str:
+    """Mangled name of the attention kernel a tile resolves to (the key of kernel_resources.json),
+    as the library resolves it; needs no device."""
+    return _kernel_symbol(0, variant, dtype, D, tile, None)
 
 
 def gemm_kernel_symbol(tile: GemmTile) -> str:
-    wm = 2  # every built GEMM tile splits its waves 2 x (waves / 2)
-    wn = tile.waves // wm
-    return (
-        f"_ZN2fa15gemm_f16_kernelILi{tile.block_m}ELi{tile.block_n}ELi{tile.block_k}ELi{wm}ELi{wn}EEEvNS_10GemmParamsE"
-    )
+    """Mangled name of the GEMM kernel a tile runs (its default deep-ring kernel); needs no device."""
+    return _kernel_symbol(1, 0, torch.float16, 0, None, tile)

@@ -18,6 +18,7 @@
  *   gemm_f16                           <- _matmul_contiguous_kernel[grid](a,b,c,M,N,K,...)  mma.py:8-21
  *   fa_device_limits                   <- get_sm_resource_limits()                         exceptions.py:760-775
  *   fa_kernel_resources                <- Triton compile metadata (shared, n_regs)          tuner.py:341-376
+ *   fa_kernel_symbol                   <- the compiled kernel that metadata belongs to      tuner.py:356-357
  *   fa_fwd_noalloc                     (no counterpart: fa_fwd for callers that cannot allocate)
  */
 #ifndef FA_GFX950_H
@@ -29,7 +30,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 enum {
   FA_OK = 0,
@@ -182,6 +183,14 @@ int gemm_f16_supported(const gemm_tile* tile);
  * Needs a device (hipFuncGetAttributes). */
 int fa_kernel_resources(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
                         const gemm_tile* gtile, fa_resources* out);
+
+/* Mangled symbol of the kernel fa_kernel_resources describes for the same arguments (the name
+ * under which the compiler's resource report and profiler traces list it), NUL-terminated into
+ * buf[0..buf_bytes). The tuner uses it to match its candidates to those rows (the reference's
+ * tuner reads the compiled kernel's registers and shared memory, tuner.py:341-376).
+ * Needs no device. FA_EINVAL when the buffer is too small. */
+int fa_kernel_symbol(int32_t op, int32_t variant, int32_t dtype, int32_t D, const fa_tile* tile,
+                     const gemm_tile* gtile, char* buf, int32_t buf_bytes);
 
 int fa_device_limits(int32_t device, fa_device_limits_t* out);
 

@@ -72,6 +72,24 @@ def test_supported_tiles():
     assert not hip_lib.gemm_supported(hip_lib.GemmTile(96, 256, 64, 4, 8))
 
 
+def test_kernel_symbols_key_the_resource_table():
+    """fa_kernel_symbol names the kernel a tile resolves to, without a device: each built GEMM tile
+    and a pipelined attention tile map to a row of the compiler's resource table; a buffer too small
+    for the name is rejected, an unbuilt tile is unsupported."""
+    table = hip_lib.compiled_resources()
+    for t in ((256, 256, 64, 8), (256, 256, 32, 8), (256, 256, 64, 4), (128, 128, 32, 4), (64, 256, 32, 4)):
+        sym = hip_lib.gemm_kernel_symbol(hip_lib.GemmTile(*t, 8))
+        assert sym.startswith(f"_ZN2fa15gemm_f16_kernelILi{t[0]}ELi{t[1]}ELi{t[2]}E") and sym in table, sym
+    fsym = hip_lib.fwd_kernel_symbol(hip_lib.FA_VARIANT_OPT, torch.float16, 128, hip_lib.make_tile(128, 64, 4, 3))
+    assert fsym in table and "ELi64ELi3ELb0E" in fsym
+    lib = hip_lib.load()
+    small = ctypes.create_string_buffer(8)
+    tile = hip_lib.GemmTile(256, 256, 64, 8, 8)
+    assert lib.fa_kernel_symbol(1, 0, 0, 0, None, ctypes.byref(tile), small, len(small)) == hip_lib.FA_EINVAL
+    assert lib.fa_kernel_symbol(1, 0, 0, 0, None, ctypes.byref(hip_lib.GemmTile(96, 256, 64, 4, 8)), small,
+                                len(small)) == hip_lib.FA_ENOTSUP
+
+
 def _args(**over):
     a = hip_lib.FaFwdArgs()
     a.q = a.k = a.v = a.o = 256  # never dereferenced: every case below fails validation first

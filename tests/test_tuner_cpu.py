@@ -337,3 +337,25 @@ def test_every_candidate_has_compiled_resources():
                     assert f"ELi{c.block_n}ELi{c.stages}ELb" in sym, (sym, c)
     for t in cfgs.gemm_candidates():
         assert cfgs.gemm_resources(t) is not None
+
+
+def test_refine_reranks_the_top_candidates_by_interleaved_medians(monkeypatch):
+    """gfx950_tune._refine re-times only the fastest three of a first pass, in interleaved rounds,
+    and ranks them by their medians (a one-pass outlier does not win the table)."""
+    import gfx950_tune
+    first = {"a": 1.00, "b": 1.01, "c": 1.02, "d": 1.50}
+    later = {"a": [1.10, 1.09, 1.11, 1.10, 1.30], "b": [1.00, 1.01, 1.00, 0.99, 1.00], "c": [1.05] * 5}
+    calls = []
+
+    def fake_time(fn, warmup, iters, batch_ms=1.0):
+        key = fn()
+        calls.append(key)
+        return later[key][sum(1 for k in calls if k == key) - 1]
+
+    monkeypatch.setattr(gfx950_tune, "_time", fake_time)
+    fns = {k: (lambda k=k: k) for k in first}
+    refined = gfx950_tune._refine(fns, first)
+    assert set(refined) == {"a", "b", "c"} and "d" not in calls
+    assert calls[:3] == ["a", "b", "c"]  # interleaved, not candidate after candidate
+    assert min(refined, key=refined.get) == "b" and refined["a"] == 1.10
+    assert gfx950_tune._refine({"a": fns["a"]}, {"a": 1.0}) == {}
