@@ -44,8 +44,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 const fa::FaKernelEntry* find_fwd(int stages, int dtype, int D, int waves, int rows_per_wave, int block_n,
                                   int split) {
+  // stages 1-5: fa_fwd.hip (32x32x16 MFMAs); stages 6-7: fa_fwd16.hip (16x16x32 MFMAs)
   int n = 0;
-  const fa::FaKernelEntry* e = fa::fa_fwd_registry(&n);
+  const fa::FaKernelEntry* e = stages >= 6 ? fa::fa_fwd16_registry(&n) : fa::fa_fwd_registry(&n);
   for (int i = 0; i < n; ++i)
     if (e[i].stages == stages && e[i].dtype == dtype && e[i].D == D && e[i].waves == waves &&
         e[i].rows_per_wave == rows_per_wave && e[i].block_n == block_n && e[i].split == split)
@@ -76,7 +77,7 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 // two-tile-ahead pipeline).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
-  return (t != nullptr && (t->stages == 3 || t->stages == 4 || t->stages == 5)) ? t->stages : 2;
+  return (t != nullptr && t->stages >= 3 && t->stages <= 7) ? t->stages : 2;
 }
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.

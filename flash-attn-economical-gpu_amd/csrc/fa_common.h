@@ -34,6 +34,10 @@ struct DT<f16_t> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
                                                   __builtin_bit_cast(half8, b), c, 0, 0, 0);
   }
+  __device__ static inline floatx4 mfma16(const u32x4& a, const u32x4& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  }
   // Two fp32 -> packed pair of binary16 (round to nearest even), low half = x.
   __device__ static inline uint32_t pack2(float x, float y) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -55,6 +59,10 @@ struct DT<bf16_t> {
   typedef bf16x8 vec8;
   __device__ static inline floatx16 mfma32(const u32x4& a, const u32x4& b, const floatx16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline floatx4 mfma16(const u32x4& a, const u32x4& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float x, float y) {
@@ -92,7 +100,52 @@ __device__ inline float xhalf_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16-lane rows of a wave that hold
+// one column of a 16x16 MFMA tile): v_permlane32_swap, then v_permlane16_swap, which swaps the odd
+// 16-lane rows of one copy with the even rows of another.
+__device__ inline float xquad_max(float x) {
+  const float h = xhalf_max(x);
+  const uint32_t u = __float_as_uint(h);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float xquad_sum(float x) {
+  const float h = xhalf_sum(x);
+  const uint32_t u = __float_as_uint(h);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+#define FA_NEG_INF (-__builtin_inff())
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// 4 x 16-bit transposing LDS read (ds_read_b64_tr_b16), returned as two dwords: in each 16-lane
+// group, lane L addresses 4 elements of row L >> 2 at columns 4 (L & 3) .. +3 of a 4 x 16 block,
+// and result lane i holds column i of the 4 rows.
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// acc + the two 16-bit values of `packed` (v_dot2 with (1, 1)).
+template <typename Tag>
+__device__ inline float dot2_sum(uint32_t packed, float acc);
+template <>
+__device__ inline float dot2_sum<f16_t>(uint32_t packed, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, packed), (h2){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+template <>
+__device__ inline float dot2_sum<bf16_t>(uint32_t packed, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, packed), (b2){(__bf16)1.0f, (__bf16)1.0f}, acc,
+                                         false);
+}
 
 // Raw buffer resource (the four descriptor words) over [base, base + bytes): buffer loads address
 // it with a 32-bit per-lane byte offset and return zeros for offsets at or past `bytes` (the

@@ -44,31 +44,6 @@
 
 namespace fa {
 
-#define FA_NEG_INF (-__builtin_inff())
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// 4 x 16-bit transposing LDS read (see the header comment), returned as two dwords.
-__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
-  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
-
-template <typename Tag>
-__device__ inline float dot2_sum(uint32_t packed, float acc);
-template <>
-__device__ inline float dot2_sum<f16_t>(uint32_t packed, float acc) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, packed), (h2){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
-}
-template <>
-__device__ inline float dot2_sum<bf16_t>(uint32_t packed, float acc) {
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, packed), (b2){(__bf16)1.0f, (__bf16)1.0f}, acc,
-                                         false);
-}
-
 template <typename Tag, int D, int WAVES, int RT, int BN, int STAGES, bool SPLIT>
 struct FwdKernel {
   static constexpr int THREADS = WAVES * 64;

@@ -1,0 +1,491 @@
+// Attention forward with v_mfma_f32_16x16x32 tiles (stages=6): the lean one-KV-tile-per-step
+// pipeline (stages=5) rebuilt around 16x16 MFMA tiles.
+//
+// Same algorithm as fa_fwd.hip (reference flash_atten.py:14-50 / 136-172 / 261-275: online
+// softmax over KV tiles in the exp2 domain with a lazily moved row offset, P rounded to the input
+// dtype before P V, O normalised by the row sum at the end; causal top-left; GQA by head index;
+// split-KV partials + LSE merge for the sliced variant). What changes is the matrix-core shape:
+//  * 16x16x32 MFMAs move half the accumulator registers per flop of 32x32x16 ones. The attention
+//    kernels run at the chip's power cap (MFMA busy ~0.6 at 1.5-1.7 GHz); in the GEMM the same
+//    switch raised the clock of the power-capped 8-wave tiles from ~1.5 to ~1.8 GHz.
+//  * Scores are S^T = K Q^T per 16-key x 16-query tile: lane l holds query (l & 15) and keys
+//    4 (l >> 4) + 0..3, so a query's row max / sum spans the four 16-lane rows of the wave (two
+//    permlane swaps). Each wave owns 32 query rows as two 16-query tiles.
+//  * P feeds P V straight from the score registers. For 32 keys (score tiles 2c, 2c+1) a lane holds
+//    keys {4g .. 4g+3} and {16+4g .. 16+4g+3} (g = l >> 4) of its query: those 8 values are its B
+//    operand (MFMA k index 8g + e), and the V^T A operand is built to match: two transposing reads
+//    whose 16-lane group g addresses rows 4g.. and 16+4g.. of the 32-key chunk.
+//  * K and V tiles reach LDS by LDS-DMA in fragment-major order (every 1 KiB block is exactly what
+//    one read instruction of the wave reads), into a 2-slot ring, as in stages=5.
+#include "fa_common.h"
+#include "fa_kernels.h"
+#include "../../include/fa_gfx950.h"
+
+namespace fa {
+
+// PIPE 0 (stages=6): one KV tile per step. PIPE 1 (stages=7): the stages=3 software pipeline --
+// the QK MFMAs of tile u+1 beside the exp / pack VALU work of tile u, then the PV MFMAs of tile u
+// beside the row max of tile u+1.
+template <typename Tag, int D, int WAVES, int BN, int PIPE, bool SPLIT>
+struct Fwd16 {
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int QT = 2;            // 16-query tiles per wave
+  static constexpr int ROWS = 16 * QT;    // query rows per wave
+  static constexpr int BM = WAVES * ROWS;
+  static constexpr int DC = D / 32;       // 32-deep d chunks of Q K^T
+  static constexpr int DTL = D / 16;      // 16-row d tiles of O^T
+  static constexpr int JT = BN / 16;      // 16-key score tiles
+  static constexpr int KC = BN / 32;      // 32-key chunks of P V
+  static constexpr int NKB = JT * DC;     // 1 KiB K blocks per tile
+  static constexpr int NVB = KC * DTL;    // 1 KiB V blocks per tile
+  static constexpr int KT_ELEMS = NKB * 512;
+  static constexpr int VT_ELEMS = NVB * 512;
+  static constexpr int NKW = NKB / WAVES;  // DMA blocks per wave per tile
+  static constexpr int NVW = NVB / WAVES;
+  static constexpr float THRESH = 8.0f;    // lazy-rescale threshold (log2 units)
+  static constexpr bool kSumRounded = __is_same(Tag, f16_t);
+  static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+  static_assert(NKB % WAVES == 0 && NVB % WAVES == 0, "tile blocks must split evenly over waves");
+  static_assert(DC % NKW == 0 && DTL % NVW == 0, "a wave's DMA blocks stay in one key group");
+  static_assert(BM % BN == 0, "causal tile bound assumes block_m % block_n == 0");
+  // Workgroups per CU the launch bounds ask for: the one-tile-per-step kernel with 32-key tiles at
+  // D <= 128 fits three (LDS and registers), the others two (the pipelined kernel holds two score
+  // tiles).
+  static constexpr int kBlocksPerCu = (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
+
+  typedef DT<Tag> T;
+  typedef floatx4 STile[JT][QT];
+  typedef floatx4 OAcc[DTL][QT];
+
+  // S^T tiles of one KV tile from its fragment-major K slot: block (jt, cc) holds, at byte 16 l,
+  // K[jt*16 + (l & 15)][cc*32 + 8 (l >> 4) .. +7] (the MFMA A operand of lane l).
+  __device__ static inline void qk(STile& s, const u32x4 (&qf)[QT][DC], const uint16_t* kslot_lane) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[jt][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc) {
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(kslot_lane + (jt * DC + cc) * 512);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) s[jt][qt] = T::mfma16(kf, qf[qt][cc], s[jt][qt]);
+      }
+    }
+  }
+
+  // O^T += V^T P^T from the fragment-major V slot: block (kc, dt) holds the two transposing reads of
+  // that (32-key chunk, 16-column d tile); in read `half` lane L's 8 bytes (at 8 L) are
+  // V[kc*32 + 16 half + 4 (L >> 4) + ((L & 15) >> 2)][dt*16 + 4 (L & 3) .. +3].
+  __device__ static inline void pv(OAcc& acc, const u32x4 (&pk)[KC][QT], const uint16_t* vslot_lane) {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) {
+        const uint16_t* base = vslot_lane + (kc * DTL + dt) * 512;
+        const u32x2 lo = lds_read_tr16(base);
+        const u32x2 hi = lds_read_tr16(base + 256);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) acc[dt][qt] = T::mfma16(vf, pk[kc][qt], acc[dt][qt]);
+      }
+    }
+  }
+
+  // Keys past N, and (causal) keys after the query row, get score -inf. Wave-uniform test first.
+  __device__ static inline bool tile_needs_mask(int n0, int wrow0, const FwdParams& p) {
+    return (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
+  }
+  __device__ static inline void mask_tile(STile& s, int n0, int wrow0, int q16, int g, const FwdParams& p) {
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int i = wrow0 + qt * 16 + q16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = n0 + jt * 16 + 4 * g + r;
+          if (j >= p.N || (p.causal && j > i)) s[jt][qt][r] = FA_NEG_INF;
+        }
+      }
+  }
+
+  // Row max of a score tile over the four lane rows holding each query.
+  __device__ static inline void tile_max(const STile& s, float (&mx)[QT]) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float m = FA_NEG_INF;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+        m = fmaxf(m, fmaxf(fmaxf(s[jt][qt][0], s[jt][qt][1]), fmaxf(s[jt][qt][2], s[jt][qt][3])));
+      mx[qt] = xquad_max(m);
+    }
+  }
+
+  // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some row of the
+  // wave sees a max more than THRESH (log2 units) above it.
+  __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, float (&m_use)[QT], float (&l_i)[QT],
+                                        float c) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const bool need = mx[qt] > m_use[qt] + THRESH / c;
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float m_new = fmaxf(m_use[qt], mx[qt]);
+        const float alpha = (m_use[qt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[qt] - m_new) * c);
+        m_use[qt] = m_new;
+        l_i[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[dt][qt][r] *= alpha;
+      }
+    }
+  }
+
+  // Online softmax of one score tile: masks where needed, row max, lazy rescale, then P.
+  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][QT], OAcc& acc, float (&m_use)[QT],
+                                        float (&l_i)[QT], int n0, int wrow0, int q16, int g, const FwdParams& p) {
+    if (tile_needs_mask(n0, wrow0, p)) mask_tile(s, n0, wrow0, q16, g, p);
+    float mx[QT];
+    tile_max(s, mx);
+    rescale(mx, acc, m_use, l_i, p.c);
+    exp_pack(s, pk, m_use, l_i, p.c);
+  }
+
+  // P = exp2(S c - m_use c) rounded to the input dtype and packed as the B operand of P V; the row
+  // sum l accumulates the same P.
+  __device__ static inline void exp_pack(const STile& s, u32x4 (&pk)[KC][QT], const float (&m_use)[QT],
+                                         float (&l_i)[QT], float c) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float mc = (m_use[qt] == FA_NEG_INF) ? 0.f : m_use[qt] * c;
+      float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const floatx4& t = s[2 * kc + half][qt];
+            const float e0 = fast_exp2(__builtin_fmaf(t[2 * w], c, -mc));
+            const float e1 = fast_exp2(__builtin_fmaf(t[2 * w + 1], c, -mc));
+            const uint32_t pw = T::pack2(e0, e1);
+            pk[kc][qt][2 * half + w] = pw;
+            if (kSumRounded) {
+              // binary16 P: summing the rounded pair moves l by <= 2^-12 relative
+              if (w) l1 = dot2_sum<Tag>(pw, l1);
+              else l0 = dot2_sum<Tag>(pw, l0);
+            } else {
+              // bfloat16 P is too coarse for l: sum the fp32 values
+              if (w) l1 += e0 + e1;
+              else l0 += e0 + e1;
+            }
+          }
+      l_i[qt] += l0 + l1;
+    }
+  }
+
+  // Scheduling hints: LDS fragment reads a few MFMAs ahead of their use.
+  __device__ static inline void qk_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < DC * JT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+    }
+  }
+  __device__ static inline void pv_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+    for (int i = 0; i < KC * DTL; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+  }
+  // Pipelined step, first half: the next tile's QK MFMAs with this tile's exp / pack / sum VALU work
+  // (FMA + exp per score, pack + sum per pair), a few VALU ops per group of QT MFMAs.
+  static constexpr int kExpValu = QT * JT * (4 * 2 + 2 * 2);
+  static constexpr int kXValuPerMfma = (kExpValu + DC * JT - 1) / (DC * JT);
+  __device__ static inline void x_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
+#pragma unroll
+    for (int i = 0; i < DC * JT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, kXValuPerMfma, 2);
+    }
+  }
+  // Second half: this tile's PV MFMAs with the next tile's row max.
+  __device__ static inline void y_schedule() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
+#pragma unroll
+    for (int i = 0; i < KC * DTL; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
+    }
+  }
+
+  __device__ static void run(const FwdParams& p) {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (KT_ELEMS + VT_ELEMS)];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q16 = lane & 15, g = lane >> 4;
+
+    // Logical block id: XCD-local, then (bh, split, m-block), m-block fastest; packed GQA rows for
+    // decode shapes (row r = query head h + r / M, position r % M), as in fa_fwd.hip.
+    const int pid = xcd_remap(blockIdx.x, p.total_blocks);
+    int mb = pid % p.m_blocks;
+    const int rest = pid / p.m_blocks;
+    const int split = rest % p.splits;
+    const int bh = rest / p.splits;
+    if (p.causal) mb = p.m_blocks - 1 - mb;  // heaviest query blocks first
+    int b, h, hk;
+    if (p.pack > 1) {
+      b = bh / p.Hkv;
+      hk = bh % p.Hkv;
+      h = hk * p.group;
+    } else {
+      b = bh / p.H;
+      h = bh % p.H;
+      hk = h / p.group;
+    }
+    const int rows = p.M * p.pack;
+    const int m0 = mb * BM;
+    const int wrow0 = m0 + wave * ROWS;
+    const bool wave_has_rows = wrow0 < rows;
+    auto row_head = [&](int r) { return p.pack > 1 ? h + r / p.M : h; };
+    auto row_pos = [&](int r) { return p.pack > 1 ? r % p.M : r; };
+
+    // Q^T fragments (B operand of Q K^T): lane holds query row wrow0 + 16 qt + q16 at
+    // d = 32 cc + 8 g .. +7.
+    u32x4 qf[QT][DC];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int row = wrow0 + qt * 16 + q16;
+      const uint16_t* qrow =
+          p.q + (int64_t)b * p.sq0 + (int64_t)row_head(row) * p.sq1 + (int64_t)row_pos(row) * p.sq2;
+#pragma unroll
+      for (int cc = 0; cc < DC; ++cc) {
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (row < rows) val = *reinterpret_cast<const u32x4*>(qrow + cc * 32 + g * 8);
+        qf[qt][cc] = val;
+      }
+    }
+
+    // KV tiles of this split, clipped by the causal diagonal.
+    const int t_begin = split * p.tiles_per_split;
+    int n_end = (t_begin + p.tiles_per_split) * BN;
+    if (n_end > p.N) n_end = p.N;
+    if (p.causal && n_end > m0 + BM) n_end = m0 + BM;
+    const int t_end = (n_end + BN - 1) / BN;
+    const int ntiles = t_end > t_begin ? t_end - t_begin : 0;
+
+    OAcc acc;
+    float m_use[QT], l_i[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      m_use[qt] = FA_NEG_INF;
+      l_i[qt] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < DTL; ++dt) acc[dt][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    }
+
+    // LDS-DMA sources: the buffer range is the (b, kv-head) rows [0, N) of K and of V, so rows past
+    // N read as zero (the host keeps (N + block_n) * row stride * 2 bytes below 2^32). Lane m of a
+    // K block (jt, cc) moves K[jt*16 + (m & 15)][cc*32 + 8 (m >> 4) .. +7]; a wave's next block is
+    // the next d chunk (+64 bytes). Lane m of a V block (kc, dt) moves the 16 bytes of transposing-
+    // read lanes L = 2 (m & 31), L + 1 of read m >> 5: V[kc*32 + 16 (m >> 5) + 4 ((m & 31) >> 3)
+    // + ((m & 7) >> 1)][dt*16 + 8 (m & 1) .. +7]; a wave's next block is the next d tile (+32 bytes).
+    const auto krs = make_rsrc(p.k + (int64_t)b * p.sk0 + (int64_t)hk * p.sk1, (uint32_t)p.N * (uint32_t)p.sk2 * 2u);
+    const auto vrs = make_rsrc(p.v + (int64_t)b * p.sv0 + (int64_t)hk * p.sv1, (uint32_t)p.N * (uint32_t)p.sv2 * 2u);
+    uint32_t koff, voff;
+    {
+      const int blk = wave * NKW, jt = blk / DC, cc = blk % DC;
+      const uint32_t row = jt * 16 + (lane & 15), c0 = cc * 32 + 8 * (lane >> 4);
+      koff = (row * (uint32_t)p.sk2 + c0) * 2u;
+    }
+    {
+      const int blk = wave * NVW, kc = blk / DTL, dt = blk % DTL;
+      const int m = lane;
+      const uint32_t row = kc * 32 + 16 * (m >> 5) + 4 * ((m & 31) >> 3) + ((m & 7) >> 1);
+      const uint32_t c0 = dt * 16 + 8 * (m & 1);
+      voff = (row * (uint32_t)p.sv2 + c0) * 2u;
+    }
+    uint16_t* kring = smem;
+    uint16_t* vring = smem + 2 * KT_ELEMS;
+    const uint32_t kring_lds = lds_address(smem), vring_lds = kring_lds + 2 * KT_ELEMS * 2;
+    auto issue_k = [&](int u) {
+      if (u >= ntiles) return;
+      const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
+      const uint32_t slot = kring_lds + (uint32_t)(u & 1) * (KT_ELEMS * 2);
+      buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + toff, slot + wave * NKW * 1024);
+    };
+    auto issue_v = [&](int u) {
+      if (u >= ntiles) return;
+      const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
+      const uint32_t slot = vring_lds + (uint32_t)(u & 1) * (VT_ELEMS * 2);
+      buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + toff, slot + wave * NVW * 1024);
+    };
+    const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
+    const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
+
+    if constexpr (PIPE) {
+      // Step u reads K_{u+1} and V_u: K runs one tile ahead of V. 2-slot rings: step u issues
+      // K_{u+2} into K_u's slot and V_{u+1} into V_{u-1}'s (both read in step u-1) and waits for
+      // them at the end of the step. Before step u the wave holds S_u and its unmasked row max.
+      STile sa, sb;
+      float mxa[QT], mxb[QT];
+      if (ntiles > 0) {
+        issue_k(0);
+        issue_v(0);
+        issue_k(1);
+        wait_vm_lds_barrier<0>();
+        if (wave_has_rows) {
+          qk(sa, qf, klane);
+          qk_schedule();
+          tile_max(sa, mxa);
+        }
+        wait_vm_lds_barrier<0>();  // every wave is done with K slot 0 before step 0 refills it
+      }
+      // Masks for tile u (rare: sequence end, causal diagonal) and the row max they change.
+      auto fix_masked = [&](STile& cur, float (&mx_cur)[QT], int u) {
+        const int n0 = (t_begin + u) * BN;
+        if (tile_needs_mask(n0, wrow0, p)) {
+          mask_tile(cur, n0, wrow0, q16, g, p);
+          tile_max(cur, mx_cur);
+        }
+      };
+      auto step = [&](STile& cur, float (&mx_cur)[QT], STile& nxt, float (&mx_nxt)[QT], int u) {
+        issue_k(u + 2);
+        issue_v(u + 1);
+        if (wave_has_rows) {  // waves without rows still move their share of K/V
+          fix_masked(cur, mx_cur, u);
+          rescale(mx_cur, acc, m_use, l_i, p.c);
+          u32x4 pk[KC][QT];
+          exp_pack(cur, pk, m_use, l_i, p.c);
+          qk(nxt, qf, klane + ((u + 1) & 1) * KT_ELEMS);
+          x_schedule();
+          pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+          tile_max(nxt, mx_nxt);
+          y_schedule();
+        }
+        wait_vm_lds_barrier<0>();
+      };
+      auto last = [&](STile& cur, float (&mx_cur)[QT], int u) {
+        if (!wave_has_rows) return;
+        fix_masked(cur, mx_cur, u);
+        rescale(mx_cur, acc, m_use, l_i, p.c);
+        u32x4 pk[KC][QT];
+        exp_pack(cur, pk, m_use, l_i, p.c);
+        pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+        pv_schedule();
+      };
+      if (ntiles > 0) {
+        int u = 0;
+        for (; u + 2 < ntiles; u += 2) {
+          step(sa, mxa, sb, mxb, u);
+          step(sb, mxb, sa, mxa, u + 1);
+        }
+        if (u + 1 < ntiles) {
+          step(sa, mxa, sb, mxb, u);
+          last(sb, mxb, u + 1);
+        } else {
+          last(sa, mxa, u);
+        }
+      }
+    } else {
+    // One KV tile per step: step u issues tile u+1 into the slot tile u-1 left (read in step u-1)
+    // and waits for it at the end of the step.
+    if (ntiles > 0) {
+      issue_k(0);
+      issue_v(0);
+      wait_vm_lds_barrier<0>();
+    }
+    for (int u = 0; u < ntiles; ++u) {
+      issue_k(u + 1);
+      issue_v(u + 1);
+      if (wave_has_rows) {  // waves without rows still move their share of K/V
+        STile s;
+        u32x4 pk[KC][QT];
+        qk(s, qf, klane + (u & 1) * KT_ELEMS);
+        qk_schedule();
+        softmax(s, pk, acc, m_use, l_i, (t_begin + u) * BN, wrow0, q16, g, p);
+        pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+        pv_schedule();
+      }
+      wait_vm_lds_barrier<0>();
+    }
+    }
+
+    // Epilogue: l over the four lane rows, O = acc / l; lane holds d = 16 dt + 4 g .. +3.
+    constexpr float kLn2 = 0.69314718055994530942f;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float l = xquad_sum(l_i[qt]);
+      const int i = wrow0 + qt * 16 + q16;
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      const float lse_val = (l > 0.f) ? (m_use[qt] * p.c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      if (i < rows) {
+        const int hr = row_head(i), mr = row_pos(i);
+        if (SPLIT) {
+          const int64_t wrow = (int64_t)(split * p.B + b) * p.H + hr;  // [split][b][h][m] rows
+          float* wo = p.ws_o + (wrow * p.M + mr) * D;
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            floatx4 val = {acc[dt][qt][0] * inv, acc[dt][qt][1] * inv, acc[dt][qt][2] * inv, acc[dt][qt][3] * inv};
+            *reinterpret_cast<floatx4*>(wo + dt * 16 + 4 * g) = val;
+          }
+          if (g == 0) p.ws_lse[wrow * p.M + mr] = lse_val;
+        } else {
+          uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)hr * p.so1 + (int64_t)mr * p.so2;
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
+                         T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+          }
+          if (p.lse != nullptr && g == 0)
+            p.lse[(int64_t)b * p.sl0 + (int64_t)hr * p.sl1 + (int64_t)mr * p.sl2] = lse_val;
+        }
+      }
+    }
+  }
+};
+
+template <typename Tag, int D, int WAVES, int BN, int PIPE, bool SPLIT>
+__global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::kBlocksPerCu)) void fa_fwd16_kernel(
+    FwdParams p) {
+  Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run(p);
+}
+
+// Registry (stages=6: PIPE 0, stages=7: PIPE 1; 32 query rows per wave).
+#define FA16_SYM_TAG_f16_t "5f16_t"
+#define FA16_SYM_TAG_bf16_t "6bf16_t"
+#define FA16_SYMBOL(TAG, D, W, BN, PI, SP)                                                                    \
+  "_ZN2fa15fa_fwd16_kernelINS_" FA16_SYM_TAG_##TAG "ELi" #D "ELi" #W "ELi" #BN "ELi" #PI "ELb" #SP \
+  "EEEvNS_9FwdParamsE"
+#define FA16_ENTRY(TAG, DTYPE, D, W, BN, PI, SP)                                                         \
+  {6 + PI, DTYPE, D, W, 32, BN, SP, (const void*)&fa_fwd16_kernel<TAG, D, W, BN, PI, (SP != 0)>, \
+   FA16_SYMBOL(TAG, D, W, BN, PI, SP)}
+#define FA16_PAIR(TAG, DTYPE, D, BN, PI) FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 0), FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 1)
+#define FA16_ENTRIES(TAG, DTYPE, D)                                                             \
+  FA16_PAIR(TAG, DTYPE, D, 64, 0), FA16_PAIR(TAG, DTYPE, D, 32, 0), FA16_PAIR(TAG, DTYPE, D, 64, 1), \
+      FA16_PAIR(TAG, DTYPE, D, 32, 1)
+
+static const FaKernelEntry kFwd16Entries[] = {
+    FA16_ENTRIES(f16_t, FA_DTYPE_F16, 64),        FA16_ENTRIES(f16_t, FA_DTYPE_F16, 128),
+    FA16_ENTRIES(bf16_t, FA_DTYPE_BF16, 64),      FA16_ENTRIES(bf16_t, FA_DTYPE_BF16, 128),
+    // D = 256: one tile per step only (the pipelined kernel's two score tiles do not fit beside O
+    // and Q in 256 registers)
+    FA16_PAIR(f16_t, FA_DTYPE_F16, 256, 32, 0),   FA16_PAIR(bf16_t, FA_DTYPE_BF16, 256, 32, 0),
+};
+
+const FaKernelEntry* fa_fwd16_registry(int* count) {
+  *count = (int)(sizeof(kFwd16Entries) / sizeof(kFwd16Entries[0]));
+  return kFwd16Entries;
+}
+
+}  // namespace fa

@@ -50,6 +50,10 @@ FA_TILE_SPACE = [
     (128, 32, 4, 4),
     (128, 32, 4, 5),
     (128, 64, 4, 5),
+    (128, 64, 4, 6),
+    (128, 32, 4, 6),
+    (128, 64, 4, 7),
+    (128, 32, 4, 7),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),
@@ -67,8 +71,8 @@ FA_TILE_SPACE = [
 ]
 STAGES_BY_VARIANT = {
     hip_lib.FA_VARIANT_BASIC: (1,),
-    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 2),
-    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 2),
+    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 6, 7, 2),
+    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 6, 7, 2),
 }
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).

@@ -56,8 +56,11 @@ enum { FA_VARIANT_BASIC = 0, FA_VARIANT_OPT = 1, FA_VARIANT_SLICED = 2 };
  *   4  two-tile-ahead pipeline on the same rings: the QK^T MFMAs of tile u+2 alternate with the PV
  *      MFMAs of tile u while the softmax of tile u+1 runs;
  *   5  one tile per step on a 2-slot LDS-DMA ring, lean enough in registers for two waves per
- *      SIMD (D = 256: O and Q in VGPRs).
- *   The LDS-DMA kernels (3, 4, 5) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
+ *      SIMD (D = 256: O and Q in VGPRs);
+ *   6  the stages=5 pipeline with 16x16x32 MFMA tiles (less accumulator traffic per flop) instead
+ *      of 32x32x16 ones; 32 query rows per wave;
+ *   7  the stages=3 pipeline with 16x16x32 MFMA tiles (D <= 128).
+ *   The LDS-DMA kernels (3-7) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
  *   bytes and row strides >= D; when a launch breaks either rule, fa_fwd runs the stages=2 kernel
  *   of the same block_m and waves instead (same block_n where built, else 64). fa_fwd_supported()
  *   reports such a tile as built only when that fallback is built too. */

@@ -34,6 +34,12 @@ TILES = {
     "pipe4_128n32": (OPT, 128, 32, 4, 4),
     # one tile per step, two waves per SIMD (stages=5; D = 256)
     "lean128n32": (OPT, 128, 32, 4, 5),
+    # the stages=5 pipeline with 16x16x32 MFMA tiles (stages=6)
+    "m16_128": (OPT, 128, 64, 4, 6),
+    "m16_128n32": (OPT, 128, 32, 4, 6),
+    # 16x16x32 MFMAs with the stages=3 software pipeline (stages=7; D <= 128)
+    "m16p_128": (OPT, 128, 64, 4, 7),
+    "m16p_128n32": (OPT, 128, 32, 4, 7),
 }
 
 
@@ -100,10 +106,36 @@ CASES = [
     ("lean_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "lean128n32"),
     ("lean_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "lean128n32"),
     ("lean_d256_long_causal_gqa", 1, 4, 2, 700, 700, 256, BF16, True, "lean128n32"),
+    ("m16_d128", 1, 2, 2, 512, 512, 128, F16, False, "m16_128"),
+    ("m16_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "m16_128"),
+    ("m16_d64", 2, 2, 2, 256, 448, 64, F16, False, "m16_128"),
+    ("m16_d64_bf16_causal", 1, 3, 3, 256, 576, 64, BF16, True, "m16_128"),
+    ("m16_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "m16_128"),
+    ("m16_ragged", 2, 3, 3, 200, 333, 128, F16, False, "m16_128"),
+    ("m16_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "m16_128"),
+    ("m16_tiny", 1, 1, 1, 1, 1, 128, F16, False, "m16_128"),
+    ("m16n32_d128", 1, 2, 2, 512, 448, 128, F16, False, "m16_128n32"),
+    ("m16n32_d128_bf16_causal_ragged", 2, 2, 1, 300, 300, 128, BF16, True, "m16_128n32"),
+    ("m16n32_d256_bf16", 1, 2, 2, 256, 300, 256, BF16, False, "m16_128n32"),
+    ("m16n32_d256_f16_causal", 2, 2, 1, 200, 200, 256, F16, True, "m16_128n32"),
+    ("m16n32_d256_one_tile", 1, 1, 1, 40, 17, 256, BF16, False, "m16_128n32"),
+    ("m16n32_d256_long_causal_gqa", 1, 4, 2, 700, 700, 256, BF16, True, "m16_128n32"),
+    ("m16p_d128", 1, 2, 2, 512, 512, 128, F16, False, "m16p_128"),
+    ("m16p_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "m16p_128"),
+    ("m16p_d64", 2, 2, 2, 256, 448, 64, F16, False, "m16p_128"),
+    ("m16p_d64_bf16_causal", 1, 3, 3, 256, 576, 64, BF16, True, "m16p_128"),
+    ("m16p_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "m16p_128"),
+    ("m16p_ragged", 2, 3, 3, 200, 333, 128, F16, False, "m16p_128"),
+    ("m16p_ragged_causal", 1, 2, 1, 190, 190, 128, F16, True, "m16p_128"),
+    ("m16p_tiny", 1, 1, 1, 1, 1, 128, F16, False, "m16p_128"),
+    ("m16pn32_d128", 1, 2, 2, 512, 448, 128, F16, False, "m16p_128n32"),
+    ("m16pn32_d128_bf16_causal_ragged", 2, 2, 1, 300, 300, 128, BF16, True, "m16p_128n32"),
+    ("m16pn32_d64_causal", 1, 2, 2, 333, 333, 64, F16, True, "m16p_128n32"),
 ]
 
 
-@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32", "lean128n32"])
+@pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32", "lean128n32", "m16_128",
+                                       "m16_128n32", "m16p_128"])
 @pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320, 384, 448, 512])
 def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     """1..8 KV tiles: the pipelined loops' prologues, unrolled pairs, peeled tails (stages=4: 1, 2
@@ -145,7 +177,7 @@ def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
     B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, BF16
     print(f"[fa_abi] sliced pipelined splits={splits} causal={causal}", flush=True)
     q, k, v = make_qkv(78, B, H, Hkv, M, N, D, dtype)
-    for tile_name in ("pipe128", "pipe256", "pipe4_128"):
+    for tile_name in ("pipe128", "pipe256", "pipe4_128", "m16_128", "m16p_128"):
         o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES[tile_name], causal=causal, dtype=dtype, splits=splits)
         o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
         assert max_abs(o, o_ref) <= ATOL[dtype], tile_name
@@ -223,7 +255,8 @@ def _strided_kv(x: np.ndarray, row_stride: int, dtype, device) -> torch.Tensor:
 @pytest.mark.parametrize("why", ["short_row_stride", "span_over_4gib"])
 @pytest.mark.parametrize("D,tile_name,dtype", [(128, "pipe128", F16), (256, "pipe128n32", BF16),
                                                (128, "pipe4_128", F16), (256, "pipe4_128n32", BF16),
-                                               (256, "lean128n32", BF16)])
+                                               (256, "lean128n32", BF16), (128, "m16_128", F16),
+                                               (256, "m16_128n32", BF16), (128, "m16p_128", F16)])
 @pytest.mark.parametrize("splits", [1, 2])
 def test_fa_pipelined_fallback(gpu, why, D, tile_name, dtype, splits):
     """A pipelined (stages=3) tile whose addressing rules a launch breaks runs the double-buffered
