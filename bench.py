@@ -252,7 +252,7 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
     fa_flops = 4.0 * B * H * D * (N * (N + 1) / 2 if cfg["causal"] else N * N)
     M_, Ng, K = GEMM_SHAPE["M"], GEMM_SHAPE["N"], GEMM_SHAPE["K"]
     kernels = {
-        "attention": ("fa_fwd_kernel", fa_flops, 4 * B * H * N * D * 2),
+        "attention": ("fa_fwd", fa_flops, 4 * B * H * N * D * 2),  # fa_fwd_kernel or fa_fwd16_kernel
         "gemm": ("gemm_f16", 2.0 * M_ * Ng * K, 2 * (M_ * K + K * Ng + M_ * Ng)),
         # hipBLASLt's kernel for the same GEMM (torch.matmul in the alternating vendor rounds; the
         # fp32 product of the parity check is a Cijk_..._S_B_ kernel and is skipped)
@@ -260,7 +260,20 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
     }
 
     def is_kernel(name: str, needle: str) -> bool:
+        if needle == "fa_fwd":
+            return "fa_fwd_kernel" in name or "fa_fwd16_kernel" in name
         return needle in name and not (needle == "Cijk_" and "_S_B_" in name)
+
+    def mfma_flop(name: str) -> int:
+        """FLOP per MFMA instruction of a kernel: 16x16x32 (our fa_fwd16 kernels, GEMM tiles built
+        with MI = 16, hipBLASLt's MI16x16 kernels) or 32x32x16."""
+        if "fa_fwd16_kernel" in name or "MI16x16" in name:
+            return 16384
+        if "gemm_f16" in name and "<" in name:
+            args = [a.strip() for a in name.split("<", 1)[1].split(">", 1)[0].split(",")]
+            if len(args) >= 6 and args[5] == "16":
+                return 16384
+        return 32768
 
     out = {}
     for key, (needle, flops, algo_bytes) in kernels.items():
@@ -292,7 +305,7 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
             "clock_ghz": cycles / secs / 1e9,
             "mfma_busy": c1["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * cycles),
             "mfma_insts": c1["SQ_INSTS_MFMA"],
-            "mfma_flop_32x32x16": c1["SQ_INSTS_MFMA"] * 32768,
+            "mfma_flop_per_inst": mfma_flop(p1["kernel"]),
             "valu_per_mfma": c1["SQ_INSTS_VALU"] / c1["SQ_INSTS_MFMA"],
             "lds_per_mfma": c1["SQ_INSTS_LDS"] / c1["SQ_INSTS_MFMA"],
             "lds_bank_conflict_rate": c1["SQ_LDS_BANK_CONFLICT"] / max(c1["SQ_LDS_IDX_ACTIVE"], 1.0),
@@ -323,6 +336,7 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
     fields = [("kernel", "kernel", "{}"), ("duration (ms, pass 1 / 2)", None, None),
               ("TFLOP/s at that duration", "tflops_at_p1_duration", "{:.0f}"), ("clock (GHz)", "clock_ghz", "{:.2f}"),
               ("MFMA busy (of SIMD-cycles)", "mfma_busy", "{:.3f}"), ("MFMA instructions", "mfma_insts", "{:.4g}"),
+              ("FLOP per MFMA instruction (16x16x32: 16384, 32x32x16: 32768)", "mfma_flop_per_inst", "{}"),
               ("VALU instructions per MFMA (MFMA included)", "valu_per_mfma", "{:.2f}"),
               ("LDS instructions per MFMA", "lds_per_mfma", "{:.2f}"), ("SALU per MFMA", "salu_per_mfma", "{:.2f}"),
               ("LDS bank-conflict cycles / LDS active", "lds_bank_conflict_rate", "{:.4f}"),

@@ -111,17 +111,18 @@ def tune_attention(table: dict, sweep=FA_SWEEP, warmup: int = 2, iters: int = 5,
                     q, k, v, o, None, sm_scale=D ** -0.5, causal=causal, variant=variant, tile=tile, workspace=ws))
                 results[key] = round(_time(fns[key], warmup, iters), 4)
             refined = _refine(fns, results)
-            results.update(refined)
-            best = min(refined or results, key=(refined or results).get)
+            pool = refined or results
+            best = min(pool, key=pool.get)
             key = cfgs.fa_table_key(variant, dtype, D, causal, B, H, M, N)
             table["fa"][key] = {
                 "tile": [int(x) for x in best.split("x")],
-                "ms": results[best],
-                "tflops": round(flops / results[best] / 1e9, 1),
+                "ms": pool[best],
+                "tflops": round(flops / pool[best] / 1e9, 1),
                 "timed": results,
+                **({"refined": refined} if refined else {}),
             }
             log(f"[tune] attention {name} B={B} M={M} N={N} causal={causal} {vname}: best {best} "
-                f"{results[best]:.3f} ms ({flops / results[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
+                f"{pool[best]:.3f} ms ({flops / pool[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
         del q, k, v, o
         torch.cuda.empty_cache()
 
@@ -144,18 +145,19 @@ def tune_gemm(table: dict, sweep=GEMM_SWEEP, warmup: int = 2, iters: int = 5, lo
         if not results:
             continue
         refined = _refine(fns, results)
-        results.update(refined)
-        best = min(refined or results, key=(refined or results).get)
+        pool = refined or results
+        best = min(pool, key=pool.get)
         tile_part, gm_part = best.split("g")
         table["gemm"][cfgs.gemm_table_key(M, N, K)] = {
             "tile": [int(x) for x in tile_part.split("x")],
             "group_m": int(gm_part),
-            "ms": results[best],
-            "tflops": round(2.0 * M * N * K / results[best] / 1e9, 1),
+            "ms": pool[best],
+            "tflops": round(2.0 * M * N * K / pool[best] / 1e9, 1),
             "timed": results,
+            **({"refined": refined} if refined else {}),
         }
-        log(f"[tune] gemm {M}x{N}x{K}: best {best} {results[best]:.3f} ms "
-            f"({2.0 * M * N * K / results[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
+        log(f"[tune] gemm {M}x{N}x{K}: best {best} {pool[best]:.3f} ms "
+            f"({2.0 * M * N * K / pool[best] / 1e9:.0f} TFLOP/s) of {len(results)}")
         del a, b, c
         torch.cuda.empty_cache()
 
