@@ -15,6 +15,8 @@
 //    keys {4g .. 4g+3} and {16+4g .. 16+4g+3} (g = l >> 4) of its query: those 8 values are its B
 //    operand (MFMA k index 8g + e), and the V^T A operand is built to match: two transposing reads
 //    whose 16-lane group g addresses rows 4g.. and 16+4g.. of the 32-key chunk.
+//  * The pipelined binary16 kernels take the row sum l from P V itself: one more MFMA per 32-key
+//    chunk and query tile, with an all-ones A operand, leaves every lane its query's sum.
 //  * K and V tiles reach LDS by LDS-DMA in fragment-major order (every 1 KiB block is exactly what
 //    one read instruction of the wave reads), into a 2-slot ring, as in stages=5.
 #include "fa_common.h"
@@ -44,6 +46,11 @@ struct Fwd16 {
   static constexpr int NVW = NVB / WAVES;
   static constexpr float THRESH = 8.0f;    // lazy-rescale threshold (log2 units)
   static constexpr bool kSumRounded = __is_same(Tag, f16_t);
+  // Pipelined binary16 kernels: the row sum l comes from one more MFMA per (32-key chunk, query
+  // tile) whose A operand is all ones, so every lane ends with its query's full sum of the rounded
+  // P (the same sum the VALU dot2 path forms) and the step's VALU work loses 16 ops. bfloat16 keeps
+  // the fp32 sum of the unrounded P.
+  static constexpr bool kSumMfma = PIPE && __is_same(Tag, f16_t);
   static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
   static_assert(NKB % WAVES == 0 && NVB % WAVES == 0, "tile blocks must split evenly over waves");
   static_assert(DC % NKW == 0 && DTL % NVW == 0, "a wave's DMA blocks stay in one key group");
@@ -60,17 +67,14 @@ struct Fwd16 {
   // S^T tiles of one KV tile from its fragment-major K slot: block (jt, cc) holds, at byte 16 l,
   // K[jt*16 + (l & 15)][cc*32 + 8 (l >> 4) .. +7] (the MFMA A operand of lane l).
   __device__ static inline void qk(STile& s, const u32x4 (&qf)[QT][DC], const uint16_t* kslot_lane) {
-#pragma unroll
-    for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) s[jt][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < DC; ++cc) {
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) {
         const u32x4 kf = *reinterpret_cast<const u32x4*>(kslot_lane + (jt * DC + cc) * 512);
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) s[jt][qt] = T::mfma16(kf, qf[qt][cc], s[jt][qt]);
+        for (int qt = 0; qt < QT; ++qt) s[jt][qt] = T::mfma16(kf, qf[qt][cc], cc == 0 ? zero : s[jt][qt]);
       }
     }
   }
@@ -78,9 +82,16 @@ struct Fwd16 {
   // O^T += V^T P^T from the fragment-major V slot: block (kc, dt) holds the two transposing reads of
   // that (32-key chunk, 16-column d tile); in read `half` lane L's 8 bytes (at 8 L) are
   // V[kc*32 + 16 half + 4 (L >> 4) + ((L & 15) >> 2)][dt*16 + 4 (L & 3) .. +3].
-  __device__ static inline void pv(OAcc& acc, const u32x4 (&pk)[KC][QT], const uint16_t* vslot_lane) {
+  __device__ static inline void pv(OAcc& acc, const u32x4 (&pk)[KC][QT], const uint16_t* vslot_lane,
+                                   floatx4 (&lsum)[QT]) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
+      if constexpr (kSumMfma) {
+        constexpr uint32_t one2 = __is_same(Tag, f16_t) ? 0x3c003c00u : 0x3f803f80u;
+        const u32x4 ones = {one2, one2, one2, one2};
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) lsum[qt] = T::mfma16(ones, pk[kc][qt], lsum[qt]);
+      }
 #pragma unroll
       for (int dt = 0; dt < DTL; ++dt) {
         const uint16_t* base = vslot_lane + (kc * DTL + dt) * 512;
@@ -123,10 +134,23 @@ struct Fwd16 {
     }
   }
 
+  // O and l of query tile qt times alpha.
+  __device__ static inline void scale_row(int qt, float alpha, OAcc& acc, float (&l_i)[QT], floatx4 (&lsum)[QT]) {
+    if constexpr (kSumMfma) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lsum[qt][r] *= alpha;
+    } else {
+      l_i[qt] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DTL; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[dt][qt][r] *= alpha;
+  }
   // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some row of the
   // wave sees a max more than THRESH (log2 units) above it.
   __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, float (&m_use)[QT], float (&l_i)[QT],
-                                        float c) {
+                                        floatx4 (&lsum)[QT], float c) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const bool need = mx[qt] > m_use[qt] + THRESH / c;
@@ -134,22 +158,19 @@ struct Fwd16 {
         const float m_new = fmaxf(m_use[qt], mx[qt]);
         const float alpha = (m_use[qt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[qt] - m_new) * c);
         m_use[qt] = m_new;
-        l_i[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DTL; ++dt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[dt][qt][r] *= alpha;
+        scale_row(qt, alpha, acc, l_i, lsum);
       }
     }
   }
 
   // Online softmax of one score tile: masks where needed, row max, lazy rescale, then P.
   __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][QT], OAcc& acc, float (&m_use)[QT],
-                                        float (&l_i)[QT], int n0, int wrow0, int q16, int g, const FwdParams& p) {
+                                        float (&l_i)[QT], floatx4 (&lsum)[QT], int n0, int wrow0, int q16, int g,
+                                        const FwdParams& p) {
     if (tile_needs_mask(n0, wrow0, p)) mask_tile(s, n0, wrow0, q16, g, p);
     float mx[QT];
     tile_max(s, mx);
-    rescale(mx, acc, m_use, l_i, p.c);
+    rescale(mx, acc, m_use, l_i, lsum, p.c);
     exp_pack(s, pk, m_use, l_i, p.c);
   }
 
@@ -172,7 +193,9 @@ struct Fwd16 {
             const float e1 = fast_exp2(__builtin_fmaf(t[2 * w + 1], c, -mc));
             const uint32_t pw = T::pack2(e0, e1);
             pk[kc][qt][2 * half + w] = pw;
-            if (kSumRounded) {
+            if (kSumMfma) {
+              // l comes from the ones-row MFMA in pv
+            } else if (kSumRounded) {
               // binary16 P: summing the rounded pair moves l by <= 2^-12 relative
               if (w) l1 = dot2_sum<Tag>(pw, l1);
               else l0 = dot2_sum<Tag>(pw, l0);
@@ -182,7 +205,7 @@ struct Fwd16 {
               else l0 += e0 + e1;
             }
           }
-      l_i[qt] += l0 + l1;
+      if (!kSumMfma) l_i[qt] += l0 + l1;
     }
   }
 
@@ -205,7 +228,7 @@ struct Fwd16 {
   }
   // Pipelined step, first half: the next tile's QK MFMAs with this tile's exp / pack / sum VALU work
   // (FMA + exp per score, pack + sum per pair), a few VALU ops per group of QT MFMAs.
-  static constexpr int kExpValu = QT * JT * (4 * 2 + 2 * 2);
+  static constexpr int kExpValu = QT * JT * (4 * 2 + 2 * (kSumMfma ? 1 : 2));
   static constexpr int kXValuPerMfma = (kExpValu + DC * JT - 1) / (DC * JT);
   __device__ static inline void x_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
@@ -285,10 +308,12 @@ struct Fwd16 {
 
     OAcc acc;
     float m_use[QT], l_i[QT];
+    floatx4 lsum[QT];  // row sums of the ones-row MFMA (kSumMfma)
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       m_use[qt] = FA_NEG_INF;
       l_i[qt] = 0.f;
+      lsum[qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dt = 0; dt < DTL; ++dt) acc[dt][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
     }
@@ -363,12 +388,12 @@ struct Fwd16 {
         issue_v(u + 1);
         if (wave_has_rows) {  // waves without rows still move their share of K/V
           fix_masked(cur, mx_cur, u);
-          rescale(mx_cur, acc, m_use, l_i, p.c);
+          rescale(mx_cur, acc, m_use, l_i, lsum, p.c);
           u32x4 pk[KC][QT];
           exp_pack(cur, pk, m_use, l_i, p.c);
           qk(nxt, qf, klane + ((u + 1) & 1) * KT_ELEMS);
           x_schedule();
-          pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+          pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
           tile_max(nxt, mx_nxt);
           y_schedule();
         }
@@ -377,10 +402,10 @@ struct Fwd16 {
       auto last = [&](STile& cur, float (&mx_cur)[QT], int u) {
         if (!wave_has_rows) return;
         fix_masked(cur, mx_cur, u);
-        rescale(mx_cur, acc, m_use, l_i, p.c);
+        rescale(mx_cur, acc, m_use, l_i, lsum, p.c);
         u32x4 pk[KC][QT];
         exp_pack(cur, pk, m_use, l_i, p.c);
-        pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+        pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
         pv_schedule();
       };
       if (ntiles > 0) {
@@ -412,8 +437,8 @@ struct Fwd16 {
         u32x4 pk[KC][QT];
         qk(s, qf, klane + (u & 1) * KT_ELEMS);
         qk_schedule();
-        softmax(s, pk, acc, m_use, l_i, (t_begin + u) * BN, wrow0, q16, g, p);
-        pv(acc, pk, vlane + (u & 1) * VT_ELEMS);
+        softmax(s, pk, acc, m_use, l_i, lsum, (t_begin + u) * BN, wrow0, q16, g, p);
+        pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
         pv_schedule();
       }
       wait_vm_lds_barrier<0>();
@@ -424,7 +449,7 @@ struct Fwd16 {
     constexpr float kLn2 = 0.69314718055994530942f;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const float l = xquad_sum(l_i[qt]);
+      const float l = kSumMfma ? lsum[qt][0] : xquad_sum(l_i[qt]);
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       const float lse_val = (l > 0.f) ? (m_use[qt] * p.c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
