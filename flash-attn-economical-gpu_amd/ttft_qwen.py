@@ -122,6 +122,29 @@ def patched_sdpa_with_gfx950(*, allow_causal: bool = True, stats: BackendUseStat
         F.scaled_dot_product_attention = original
 
 
+@contextlib.contextmanager
+def fp32_attention() -> Iterator[None]:
+    """Replace F.scaled_dot_product_attention with attention computed in float32 (q, k, v upcast,
+    torch's math backend, output cast back): the model with exact attention, the common yardstick
+    for two bf16 attention implementations."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    original = F.scaled_dot_product_attention
+
+    def replacement(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
+                    enable_gqa=False):
+        with sdpa_kernel(SDPBackend.MATH):
+            out = original(query.float(), key.float(), value.float(), attn_mask=attn_mask, dropout_p=dropout_p,
+                           is_causal=is_causal, scale=scale, enable_gqa=enable_gqa)
+        return out.to(query.dtype)
+
+    F.scaled_dot_product_attention = replacement
+    try:
+        yield
+    finally:
+        F.scaled_dot_product_attention = original
+
+
 def prefill_logits(model, input_ids: torch.Tensor) -> torch.Tensor:
     with torch.no_grad():
         out = model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
@@ -151,12 +174,16 @@ def verify_against_torch(model, input_ids: torch.Tensor, *, variant: str = "slic
     Also reported: the same comparison between torch's default SDPA backend and its math backend
     (`torch_default_vs_math_*`). bf16 activations through many layers make two correct attention
     implementations disagree by about that much, so a failed allclose next to a torch-vs-torch
-    deviation of the same size says the tolerance, not the kernel, is at its limit."""
+    deviation of the same size says the tolerance, not the kernel, is at its limit. And both bf16
+    paths against the model with float32 attention (`*_vs_fp32_attention_*`): the distance of each
+    from exact attention, on the same rule."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     reference = prefill_logits(model, input_ids).float()
     with sdpa_kernel(SDPBackend.MATH):
         reference_math = prefill_logits(model, input_ids).float()
+    with fp32_attention():
+        exact = prefill_logits(model, input_ids).float()
     stats = BackendUseStats()
     with patched_sdpa_with_gfx950(stats=stats, variant=variant, capture=capture):
         ours = prefill_logits(model, input_ids).float()
@@ -173,6 +200,11 @@ def verify_against_torch(model, input_ids: torch.Tensor, *, variant: str = "slic
         "torch_default_vs_math_allclose_rtol_atol_0p1": bool(
             torch.allclose(reference_math, reference, rtol=0.1, atol=0.1)),
         "torch_default_vs_math_max_abs_diff": float((reference_math - reference).abs().max()),
+        "ours_vs_fp32_attention_allclose_rtol_atol_0p1": bool(torch.allclose(ours, exact, rtol=0.1, atol=0.1)),
+        "ours_vs_fp32_attention_max_abs_diff": float((ours - exact).abs().max()),
+        "torch_default_vs_fp32_attention_allclose_rtol_atol_0p1": bool(
+            torch.allclose(reference, exact, rtol=0.1, atol=0.1)),
+        "torch_default_vs_fp32_attention_max_abs_diff": float((reference - exact).abs().max()),
         "logit_abs_max": float(reference.abs().max()),
         "kernel_calls": stats.calls,
     }
@@ -202,7 +234,9 @@ def run(prompt_lens: list[int], *, layers: int | None = None, seed: int = 0, var
               f"vs torch: allclose(0.1)={check['allclose_rtol_atol_0p1']} max|dlogit|={check['max_abs_diff']:.3e} "
               f"argmax_match={check['argmax_match']}; torch default vs math: "
               f"allclose(0.1)={check['torch_default_vs_math_allclose_rtol_atol_0p1']} "
-              f"max|dlogit|={check['torch_default_vs_math_max_abs_diff']:.3e}; |logit| <= "
+              f"max|dlogit|={check['torch_default_vs_math_max_abs_diff']:.3e}; vs fp32 attention: ours "
+              f"{check['ours_vs_fp32_attention_max_abs_diff']:.3e}, torch default "
+              f"{check['torch_default_vs_fp32_attention_max_abs_diff']:.3e}; |logit| <= "
               f"{check['logit_abs_max']:.2f}", flush=True)
         results.append(row)
     return results

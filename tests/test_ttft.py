@@ -41,6 +41,25 @@ def test_patch_rejects_unsupported_calls_and_restores():
     assert F.scaled_dot_product_attention is original
 
 
+def test_fp32_attention_yardstick_is_float32_sdpa_and_restores():
+    """fp32_attention() computes every SDPA call in float32 (GQA and causal passed through) and
+    returns the caller's dtype; F.scaled_dot_product_attention is restored afterwards."""
+    original = F.scaled_dot_product_attention
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn((1, 4, 33, 16), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 2, 33, 16), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, 2, 33, 16), generator=g).to(torch.bfloat16)
+    with ttft_qwen.fp32_attention():
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+    assert F.scaled_dot_product_attention is original
+    kr, vr = (t.float().repeat_interleave(2, dim=1) for t in (k, v))
+    s = (q.float() @ kr.transpose(-1, -2)) * 16 ** -0.5
+    s = s.masked_fill(torch.ones(33, 33, dtype=torch.bool).triu(1), float("-inf"))
+    ref = torch.softmax(s, dim=-1) @ vr
+    assert out.dtype == torch.bfloat16
+    assert torch.allclose(out.float(), ref.to(torch.bfloat16).float(), atol=1e-2, rtol=0)
+
+
 def test_small_model_builds_on_cpu():
     model = ttft_qwen.build_model(seed=1, device="cpu", dtype=torch.float32,
                                   overrides=dict(SMALL, hidden_size=256, intermediate_size=512, num_attention_heads=4,
@@ -108,8 +127,9 @@ def test_qwen25_1p5b_full_prefill_layers_vs_oracle(gpu):
     gfx950 kernel. Asserted: the attention output of the first, a middle and the last layer against
     the oracle on sampled rows of three heads (bf16 bound 3e-2), one kernel call per layer, and the
     final-token argmax against torch's own SDPA. Recorded (printed as one JSON line per prompt):
-    the reference's allclose(rtol=atol=0.1) on the final logits (ttft.py:415-446) and the same
-    comparison between torch's default and math SDPA backends."""
+    the reference's allclose(rtol=atol=0.1) on the final logits (ttft.py:415-446), the same
+    comparison between torch's default and math SDPA backends, and both bf16 paths (ours, torch's
+    default) against the model with float32 attention."""
     import json
 
     print("[ttft] building the 28-layer Qwen2.5-1.5B-architecture model", flush=True)
