@@ -122,7 +122,8 @@ struct Fwd16 {
       }
   }
 
-  // Row max of a score tile over the four lane rows holding each query.
+  // Max of a score tile over this lane's keys of each query (a quarter of the row: the row's max
+  // over the four lane rows is formed only when the offset moves, in rescale).
   __device__ static inline void tile_max(const STile& s, float (&mx)[QT]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -130,7 +131,7 @@ struct Fwd16 {
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt)
         m = fmaxf(m, fmaxf(fmaxf(s[jt][qt][0], s[jt][qt][1]), fmaxf(s[jt][qt][2], s[jt][qt][3])));
-      mx[qt] = xquad_max(m);
+      mx[qt] = m;
     }
   }
 
@@ -147,15 +148,16 @@ struct Fwd16 {
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[dt][qt][r] *= alpha;
   }
-  // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some row of the
-  // wave sees a max more than THRESH (log2 units) above it.
+  // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some lane of the
+  // wave sees a score more than THRESH (log2 units) above it; the moved offset is the row max over
+  // the four lane rows, so the lanes of a query keep one offset.
   __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, float (&m_use)[QT], float (&l_i)[QT],
                                         floatx4 (&lsum)[QT], float c) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const bool need = mx[qt] > m_use[qt] + THRESH / c;
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        const float m_new = fmaxf(m_use[qt], mx[qt]);
+        const float m_new = fmaxf(m_use[qt], xquad_max(mx[qt]));
         const float alpha = (m_use[qt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[qt] - m_new) * c);
         m_use[qt] = m_new;
         scale_row(qt, alpha, acc, l_i, lsum);
