@@ -73,11 +73,11 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 }
 
 // Pipeline of a launch: basic keeps one K/V buffer (1); optimized and sliced double-buffer K/V (2),
-// or, when the tile asks for stages=3 or 4, run a software-pipelined kernel (LDS-DMA ring; 4 = the
-// two-tile-ahead pipeline).
+// or, when the tile asks for stages 3-8, run that LDS-DMA kernel (3-5: 32x32x16 MFMA tiles, 6-8:
+// 16x16x32 ones; the stages doc of fa_tile in the header lists them).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
-  return (t != nullptr && t->stages >= 3 && t->stages <= 7) ? t->stages : 2;
+  return (t != nullptr && t->stages >= 3 && t->stages <= 8) ? t->stages : 2;
 }
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.

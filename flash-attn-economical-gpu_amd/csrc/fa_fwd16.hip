@@ -19,6 +19,8 @@
 //    chunk and query tile, with an all-ones A operand, leaves every lane its query's sum.
 //  * K and V tiles reach LDS by LDS-DMA in fragment-major order (every 1 KiB block is exactly what
 //    one read instruction of the wave reads), into a 2-slot ring, as in stages=5.
+#include <type_traits>
+
 #include "fa_common.h"
 #include "fa_kernels.h"
 #include "../../include/fa_gfx950.h"
@@ -58,7 +60,9 @@ struct Fwd16 {
   // Workgroups per CU the launch bounds ask for: the one-tile-per-step kernel with 32-key tiles at
   // D <= 128 fits three (LDS and registers), the others two (the pipelined kernel holds two score
   // tiles).
-  static constexpr int kBlocksPerCu = (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
+  static constexpr int kBlocksPerCu = PIPE == 2 ? 1 : (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
+  static_assert(PIPE != 2 || WAVES == 8, "the ping-pong kernel runs two groups of four waves");
+  static constexpr bool kScalarIds = BN == 64;
 
   typedef DT<Tag> T;
   typedef floatx4 STile[JT][QT];
@@ -108,18 +112,25 @@ struct Fwd16 {
   __device__ static inline bool tile_needs_mask(int n0, int wrow0, const FwdParams& p) {
     return (n0 + BN > p.N) || (p.causal && n0 + BN - 1 > wrow0);
   }
+  // Key j of query i is kept when j < lim_i = N (or min(N, i + 1) causal). Each element takes a
+  // sign-bit mask and a bitfield select -- vector ALU only: per-element compares would each hold a
+  // scalar register pair, and the scheduler hoists all 32 of them.
   __device__ static inline void mask_tile(STile& s, int n0, int wrow0, int q16, int g, const FwdParams& p) {
+    const uint32_t ninf = __float_as_uint(FA_NEG_INF);
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt)
+    for (int qt = 0; qt < QT; ++qt) {
+      const int i = wrow0 + qt * 16 + q16;
+      const int lim = p.causal ? min(p.N, i + 1) : p.N;
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int i = wrow0 + qt * 16 + q16;
+      for (int jt = 0; jt < JT; ++jt) {
+        const int rel = lim - (n0 + jt * 16 + 4 * g);  // keys r < rel of this lane are kept
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int j = n0 + jt * 16 + 4 * g + r;
-          if (j >= p.N || (p.causal && j > i)) s[jt][qt][r] = FA_NEG_INF;
+          const uint32_t keep = (uint32_t)((r - rel) >> 31);  // all ones when r < rel
+          s[jt][qt][r] = __uint_as_float((__float_as_uint(s[jt][qt][r]) & keep) | (ninf & ~keep));
         }
       }
+    }
   }
 
   // Max of a score tile over this lane's keys of each query (a quarter of the row: the row's max
@@ -228,6 +239,23 @@ struct Fwd16 {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
   }
+  // Ping-pong matrix block (QK of the next tile, then PV of this one, one scheduling region): AHEAD
+  // LDS reads first, then the remaining K and V fragment reads spread evenly over the MFMA groups.
+  template <int I, int G, int NR>
+  __device__ static inline void m_schedule_groups() {
+    if constexpr (I < G) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 3);
+      constexpr int r = (NR * (I + 1)) / G - (NR * I) / G;
+      if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 3);
+      m_schedule_groups<I + 1, G, NR>();
+    }
+  }
+  template <int AHEAD>
+  __device__ static inline void m_schedule() {
+    constexpr int reads = DC * JT + 2 * KC * DTL;
+    __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 3);
+    m_schedule_groups<0, DC * JT + KC * DTL, reads - AHEAD>();
+  }
   // Pipelined step, first half: the next tile's QK MFMAs with this tile's exp / pack / sum VALU work
   // (FMA + exp per score, pack + sum per pair), a few VALU ops per group of QT MFMAs.
   static constexpr int kExpValu = QT * JT * (4 * 2 + 2 * (kSumMfma ? 1 : 2));
@@ -277,6 +305,17 @@ struct Fwd16 {
       h = bh % p.H;
       hk = h / p.group;
     }
+    // The integer divisions above run on the vector ALU, though their results are workgroup-
+    // uniform. Declaring them uniform puts the tile bounds, and the loop's branches on them, in
+    // scalar registers: measured 1-3% faster for the 64-key kernels; the 32-key ones lose (their
+    // register allocation grows by 30-60 VGPRs), so they keep vector copies.
+    if constexpr (kScalarIds) {
+      mb = __builtin_amdgcn_readfirstlane(mb);
+      b = __builtin_amdgcn_readfirstlane(b);
+      h = __builtin_amdgcn_readfirstlane(h);
+      hk = __builtin_amdgcn_readfirstlane(hk);
+    }
+    const int split_u = kScalarIds ? __builtin_amdgcn_readfirstlane(split) : split;
     const int rows = p.M * p.pack;
     const int m0 = mb * BM;
     const int wrow0 = m0 + wave * ROWS;
@@ -301,7 +340,7 @@ struct Fwd16 {
     }
 
     // KV tiles of this split, clipped by the causal diagonal.
-    const int t_begin = split * p.tiles_per_split;
+    const int t_begin = split_u * p.tiles_per_split;
     int n_end = (t_begin + p.tiles_per_split) * BN;
     if (n_end > p.N) n_end = p.N;
     if (p.causal && n_end > m0 + BM) n_end = m0 + BM;
@@ -359,7 +398,74 @@ struct Fwd16 {
     const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
     const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
 
-    if constexpr (PIPE) {
+    if constexpr (PIPE == 2) {
+      // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1) run the same sequence of blocks, group 1
+      // one phase behind, with a workgroup barrier between phases. Blocks alternate between matrix
+      // work and softmax work -- block 0: S = Q K_0^T; block 2u+1: softmax of tile u (mask, row
+      // max, rescale, P_u); block 2u+2: S = Q K_{u+1}^T (u+1 < n) and O += P_u V_u -- so in every
+      // phase one group issues MFMAs while the other, on the same SIMDs, issues the exp/pack VALU
+      // work, and the two streams overlap instead of taking turns inside one wave.
+      // K_t and V_t live in slot t & 1 of two-slot rings. K_t is read in phases 2t (group 0) and
+      // 2t+1 (group 1), V_t in phases 2t+2 and 2t+3; phase 2s (s >= 1) refills with K_{s+1} and
+      // V_s (their slots' previous tiles were last read in phase 2s-1) and every wave waits for its
+      // own refills before the barrier that ends phase 2s+1, two phases before their first reader.
+      STile s;
+      u32x4 pk[KC][QT];
+      auto mma_block = [&](int u) {  // S = Q K_{u+1}^T, O += P_u V_u
+        // past the last tile the QK reads a stale K slot and its S is never used: one straight-line
+        // block lets the V reads start during the QK MFMAs
+        // the matrix group issues first: its MFMAs then wait for no VALU op of the softmax group
+        __builtin_amdgcn_s_setprio(1);
+        qk(s, qf, klane + ((u + 1) & 1) * KT_ELEMS);
+        pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
+        m_schedule<4>();
+        __builtin_amdgcn_s_setprio(0);
+      };
+      auto softmax_block = [&](int t) {
+        if (t < ntiles) softmax(s, pk, acc, m_use, l_i, lsum, (t_begin + t) * BN, wrow0, q16, g, p);
+      };
+      // Group G's sequence; phases 2j and 2j+1 form iteration j. The branches on G and on
+      // wave_has_rows are wave-uniform, and every wave runs the same barriers.
+      auto run_group = [&](auto G) {
+        constexpr int grp = decltype(G)::value;
+        issue_k(0);
+        wait_vm_lds_barrier<0>();
+        issue_k(1);  // K_1 and V_0 land by the end of phase 1
+        issue_v(0);
+        if (grp == 0 && wave_has_rows) {
+          qk(s, qf, klane);
+          qk_schedule();
+        }
+        wait_vm_lds_barrier<63>();
+        if (wave_has_rows) {
+          if (grp == 0) {
+            softmax_block(0);
+          } else {
+            qk(s, qf, klane);
+            qk_schedule();
+          }
+        }
+        wait_vm_lds_barrier<0>();
+        for (int j = 1; j <= ntiles; ++j) {
+          issue_k(j + 1);
+          issue_v(j);
+          if (wave_has_rows) {
+            if (grp == 0) mma_block(j - 1);
+            else softmax_block(j - 1);
+          }
+          wait_vm_lds_barrier<63>();
+          if (wave_has_rows) {
+            if (grp == 0) softmax_block(j);
+            else mma_block(j - 1);
+          }
+          wait_vm_lds_barrier<0>();
+        }
+      };
+      if (ntiles > 0) {
+        if (wave < 4) run_group(std::integral_constant<int, 0>{});
+        else run_group(std::integral_constant<int, 1>{});
+      }
+    } else if constexpr (PIPE) {
       // Step u reads K_{u+1} and V_u: K runs one tile ahead of V. 2-slot rings: step u issues
       // K_{u+2} into K_u's slot and V_{u+1} into V_{u-1}'s (both read in step u-1) and waits for
       // them at the end of the step. Before step u the wave holds S_u and its unmasked row max.
@@ -447,35 +553,42 @@ struct Fwd16 {
     }
     }
 
-    // Epilogue: l over the four lane rows, O = acc / l; lane holds d = 16 dt + 4 g .. +3.
+    // Epilogue: l over the four lane rows, O = acc / l; lane holds d = 16 dt + 4 g .. +3. The
+    // output parameters are read again from the kernel-argument segment (scalar loads) rather than
+    // kept in scalar registers across the loop, where they would crowd out its own.
+    typedef const __attribute__((address_space(4))) FwdParams* KernargParams;
+    KernargParams pe = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(pe));
     constexpr float kLn2 = 0.69314718055994530942f;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const float l = kSumMfma ? lsum[qt][0] : xquad_sum(l_i[qt]);
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
-      const float lse_val = (l > 0.f) ? (m_use[qt] * p.c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
       if (i < rows) {
-        const int hr = row_head(i), mr = row_pos(i);
+        const int hr = pe->pack > 1 ? h + i / pe->M : h;
+        const int mr = pe->pack > 1 ? i % pe->M : i;
         if (SPLIT) {
-          const int64_t wrow = (int64_t)(split * p.B + b) * p.H + hr;  // [split][b][h][m] rows
-          float* wo = p.ws_o + (wrow * p.M + mr) * D;
+          const int64_t wrow = (int64_t)(split_u * pe->B + b) * pe->H + hr;  // [split][b][h][m] rows
+          float* wo = pe->ws_o + (wrow * pe->M + mr) * D;
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt) {
             floatx4 val = {acc[dt][qt][0] * inv, acc[dt][qt][1] * inv, acc[dt][qt][2] * inv, acc[dt][qt][3] * inv};
             *reinterpret_cast<floatx4*>(wo + dt * 16 + 4 * g) = val;
           }
-          if (g == 0) p.ws_lse[wrow * p.M + mr] = lse_val;
+          if (g == 0) pe->ws_lse[wrow * pe->M + mr] = lse_val;
         } else {
-          uint16_t* orow = p.o + (int64_t)b * p.so0 + (int64_t)hr * p.so1 + (int64_t)mr * p.so2;
+          uint16_t* orow = pe->o + (int64_t)b * pe->so0 + (int64_t)hr * pe->so1 + (int64_t)mr * pe->so2;
 #pragma unroll
           for (int dt = 0; dt < DTL; ++dt) {
             u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
                          T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
             *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
           }
-          if (p.lse != nullptr && g == 0)
-            p.lse[(int64_t)b * p.sl0 + (int64_t)hr * p.sl1 + (int64_t)mr * p.sl2] = lse_val;
+          float* lse = pe->lse;
+          if (lse != nullptr && g == 0)
+            lse[(int64_t)b * pe->sl0 + (int64_t)hr * pe->sl1 + (int64_t)mr * pe->sl2] = lse_val;
         }
       }
     }
@@ -488,7 +601,8 @@ __global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>:
   Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run(p);
 }
 
-// Registry (stages=6: PIPE 0, stages=7: PIPE 1; 32 query rows per wave).
+// Registry (stages=6: PIPE 0, stages=7: PIPE 1, stages=8: PIPE 2 with 8 waves; 32 query rows per
+// wave).
 #define FA16_SYM_TAG_f16_t "5f16_t"
 #define FA16_SYM_TAG_bf16_t "6bf16_t"
 #define FA16_SYMBOL(TAG, D, W, BN, PI, SP)                                                                    \
@@ -498,9 +612,10 @@ __global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>:
   {6 + PI, DTYPE, D, W, 32, BN, SP, (const void*)&fa_fwd16_kernel<TAG, D, W, BN, PI, (SP != 0)>, \
    FA16_SYMBOL(TAG, D, W, BN, PI, SP)}
 #define FA16_PAIR(TAG, DTYPE, D, BN, PI) FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 0), FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 1)
+#define FA16_PAIR8(TAG, DTYPE, D, BN) FA16_ENTRY(TAG, DTYPE, D, 8, BN, 2, 0), FA16_ENTRY(TAG, DTYPE, D, 8, BN, 2, 1)
 #define FA16_ENTRIES(TAG, DTYPE, D)                                                             \
   FA16_PAIR(TAG, DTYPE, D, 64, 0), FA16_PAIR(TAG, DTYPE, D, 32, 0), FA16_PAIR(TAG, DTYPE, D, 64, 1), \
-      FA16_PAIR(TAG, DTYPE, D, 32, 1)
+      FA16_PAIR(TAG, DTYPE, D, 32, 1), FA16_PAIR8(TAG, DTYPE, D, 64)
 
 static const FaKernelEntry kFwd16Entries[] = {
     FA16_ENTRIES(f16_t, FA_DTYPE_F16, 64),        FA16_ENTRIES(f16_t, FA_DTYPE_F16, 128),

@@ -40,8 +40,12 @@ VARIANT_BY_KERNEL = {
 #   4  two-tile-ahead pipeline (QK of tile u+2 one for one with PV of tile u, the softmax of tile
 #      u+1 spread over both; same LDS-DMA rings),
 #   5  one tile per step in a 2-slot LDS-DMA ring, lean enough in registers for two waves per
-#      SIMD at D = 256.
-# The basic variant uses stages 1; optimized and sliced use 5, 4, 3 or 2.
+#      SIMD at D = 256,
+#   6  stages 5 with 16x16x32 MFMA tiles,
+#   7  stages 3 with 16x16x32 MFMA tiles,
+#   8  ping-pong: 8 waves in two groups of four that alternate MFMA phases and softmax phases
+#      on the same SIMDs (16x16x32 MFMA tiles, 256 query rows per workgroup).
+# The basic variant uses stages 1; optimized and sliced use 2 to 8.
 FA_TILE_SPACE = [
     (128, 64, 4, 3),
     (256, 64, 8, 3),
@@ -54,6 +58,7 @@ FA_TILE_SPACE = [
     (128, 32, 4, 6),
     (128, 64, 4, 7),
     (128, 32, 4, 7),
+    (256, 64, 8, 8),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),
@@ -71,8 +76,8 @@ FA_TILE_SPACE = [
 ]
 STAGES_BY_VARIANT = {
     hip_lib.FA_VARIANT_BASIC: (1,),
-    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 6, 7, 2),
-    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 6, 7, 2),
+    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 6, 7, 8, 2),
+    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 6, 7, 8, 2),
 }
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).

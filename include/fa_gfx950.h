@@ -59,8 +59,11 @@ enum { FA_VARIANT_BASIC = 0, FA_VARIANT_OPT = 1, FA_VARIANT_SLICED = 2 };
  *      SIMD (D = 256: O and Q in VGPRs);
  *   6  the stages=5 pipeline with 16x16x32 MFMA tiles (less accumulator traffic per flop) instead
  *      of 32x32x16 ones; 32 query rows per wave;
- *   7  the stages=3 pipeline with 16x16x32 MFMA tiles (D <= 128).
- *   The LDS-DMA kernels (3-7) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
+ *   7  the stages=3 pipeline with 16x16x32 MFMA tiles (D <= 128);
+ *   8  ping-pong (block_m 256, 8 waves, block_n 64, D <= 128): two groups of four waves, one phase
+ *      apart, alternate a matrix phase (QK^T of the next tile, PV of this one) and a softmax phase,
+ *      so that on every SIMD one wave issues MFMAs while the other issues the exp/pack work.
+ *   The LDS-DMA kernels (3-8) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
  *   bytes and row strides >= D; when a launch breaks either rule, fa_fwd runs the stages=2 kernel
  *   of the same block_m and waves instead (same block_n where built, else 64). fa_fwd_supported()
  *   reports such a tile as built only when that fallback is built too. */

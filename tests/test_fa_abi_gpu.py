@@ -40,6 +40,8 @@ TILES = {
     # 16x16x32 MFMAs with the stages=3 software pipeline (stages=7; D <= 128)
     "m16p_128": (OPT, 128, 64, 4, 7),
     "m16p_128n32": (OPT, 128, 32, 4, 7),
+    # ping-pong (stages=8): 8 waves in two groups one phase apart, 256 rows, 16x16x32 MFMAs
+    "pp_256": (OPT, 256, 64, 8, 8),
 }
 
 
@@ -131,11 +133,20 @@ CASES = [
     ("m16pn32_d128", 1, 2, 2, 512, 448, 128, F16, False, "m16p_128n32"),
     ("m16pn32_d128_bf16_causal_ragged", 2, 2, 1, 300, 300, 128, BF16, True, "m16p_128n32"),
     ("m16pn32_d64_causal", 1, 2, 2, 333, 333, 64, F16, True, "m16p_128n32"),
+    ("pp_d128", 1, 2, 2, 512, 512, 128, F16, False, "pp_256"),
+    ("pp_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "pp_256"),
+    ("pp_d64", 2, 2, 2, 256, 448, 64, F16, False, "pp_256"),
+    ("pp_d64_bf16_causal", 1, 3, 3, 300, 576, 64, BF16, True, "pp_256"),
+    ("pp_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "pp_256"),
+    ("pp_ragged", 2, 3, 3, 200, 333, 128, F16, False, "pp_256"),
+    ("pp_ragged_causal", 1, 2, 1, 290, 290, 128, F16, True, "pp_256"),
+    ("pp_idle_waves", 1, 2, 2, 40, 700, 128, F16, False, "pp_256"),  # waves 2-7 hold no rows
+    ("pp_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pp_256"),
 ]
 
 
 @pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32", "lean128n32", "m16_128",
-                                       "m16_128n32", "m16p_128"])
+                                       "m16_128n32", "m16p_128", "pp_256"])
 @pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320, 384, 448, 512])
 def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     """1..8 KV tiles: the pipelined loops' prologues, unrolled pairs, peeled tails (stages=4: 1, 2
@@ -151,7 +162,7 @@ def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     assert max_abs(lse, lse_ref) <= 1e-3
 
 
-@pytest.mark.parametrize("tile_name", ["opt256w8", "pipe128", "pipe256"])
+@pytest.mark.parametrize("tile_name", ["opt256w8", "pipe128", "pipe256", "pp_256"])
 def test_fa_strided_bshd_layout(gpu, tile_name):
     """q/k/v/o as [B, S, H, D] memory viewed as [B, H, S, D] (row stride H*D): buffer ranges and
     DMA offsets of the pipelined kernel follow the strides."""
@@ -177,7 +188,7 @@ def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
     B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, BF16
     print(f"[fa_abi] sliced pipelined splits={splits} causal={causal}", flush=True)
     q, k, v = make_qkv(78, B, H, Hkv, M, N, D, dtype)
-    for tile_name in ("pipe128", "pipe256", "pipe4_128", "m16_128", "m16p_128"):
+    for tile_name in ("pipe128", "pipe256", "pipe4_128", "m16_128", "m16p_128", "pp_256"):
         o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES[tile_name], causal=causal, dtype=dtype, splits=splits)
         o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
         assert max_abs(o, o_ref) <= ATOL[dtype], tile_name
@@ -256,7 +267,8 @@ def _strided_kv(x: np.ndarray, row_stride: int, dtype, device) -> torch.Tensor:
 @pytest.mark.parametrize("D,tile_name,dtype", [(128, "pipe128", F16), (256, "pipe128n32", BF16),
                                                (128, "pipe4_128", F16), (256, "pipe4_128n32", BF16),
                                                (256, "lean128n32", BF16), (128, "m16_128", F16),
-                                               (256, "m16_128n32", BF16), (128, "m16p_128", F16)])
+                                               (256, "m16_128n32", BF16), (128, "m16p_128", F16),
+                                               (128, "pp_256", BF16)])
 @pytest.mark.parametrize("splits", [1, 2])
 def test_fa_pipelined_fallback(gpu, why, D, tile_name, dtype, splits):
     """A pipelined (stages=3) tile whose addressing rules a launch breaks runs the double-buffered

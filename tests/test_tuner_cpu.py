@@ -334,8 +334,9 @@ def test_every_candidate_has_compiled_resources():
                     assert res is not None and res["lds_bytes"] <= 160 * 1024
                     # the resources are those of the candidate's own pipeline
                     sym = hip_lib.fwd_kernel_symbol(variant, dtype, D, c.to_c())
-                    if c.stages >= 6:  # the 16x16x32-MFMA kernels: PIPE 0 (stages 6) or 1 (stages 7)
-                        assert "fa_fwd16_kernel" in sym and f"ELi{c.block_n}ELi{c.stages - 6}ELb" in sym, (sym, c)
+                    if c.stages >= 6:  # the 16x16x32-MFMA kernels: PIPE 0, 1, 2 (stages 6, 7, 8)
+                        assert "fa_fwd16_kernel" in sym and f"ELi{c.waves}ELi{c.block_n}ELi{c.stages - 6}ELb" in sym, (
+                            sym, c)
                     else:
                         assert f"ELi{c.block_n}ELi{c.stages}ELb" in sym, (sym, c)
     for t in cfgs.gemm_candidates():
