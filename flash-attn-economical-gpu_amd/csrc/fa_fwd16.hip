@@ -62,7 +62,7 @@ struct Fwd16 {
   // tiles).
   static constexpr int kBlocksPerCu = PIPE == 2 ? 1 : (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
   static_assert(PIPE != 2 || WAVES == 8, "the ping-pong kernel runs two groups of four waves");
-  static constexpr bool kScalarIds = BN == 64;
+  static constexpr bool kScalarIds = BN == 64 && PIPE != 1;
 
   typedef DT<Tag> T;
   typedef floatx4 STile[JT][QT];

@@ -71,6 +71,36 @@ def test_selection_returns_the_table_winner(fresh_table_cache):
         assert mma._select_2d_contiguous_config(M, N, K)[:4] == (bm, bn, bk, gm)
 
 
+def test_table_timed_every_current_candidate(fresh_table_cache):
+    """Each entry was swept with every tile the library now builds for its (variant, dtype, D):
+    a table older than a newly built tile would never select it."""
+    table = cfgs.load_tune_table()
+    for key, entry in table["fa"].items():
+        variant, dtype, D, _causal, _bh, _m, _n = _parse_fa_key(key)
+        built = {f"{c.block_m}x{c.block_n}x{c.waves}x{c.stages}" for c in cfgs.fa_candidates(variant, dtype, D)}
+        assert built <= set(entry["timed"]), (key, sorted(built - set(entry["timed"])))
+    for key, entry in table["gemm"].items():
+        M, N, K = (int(p[1:]) for p in key.split("|"))
+        built = {f"{t[0]}x{t[1]}x{t[2]}x{t[3]}g{gm}" for t in cfgs.gemm_candidates()
+                 if M % t[0] == 0 and N % t[1] == 0 and K % t[2] == 0 for gm in gfx950_tune.GROUP_MS}
+        assert built <= set(entry["timed"]), (key, sorted(built - set(entry["timed"])))
+
+
+def test_selected_tiles_do_not_spill(fresh_table_cache):
+    """Every kernel the table selects (and, for the sliced variant, its split instantiation)
+    compiles without scratch: a spill inside the KV loop costs HBM traffic on every step."""
+    table = cfgs.load_tune_table()
+    for key, entry in table["fa"].items():
+        variant, dtype, D, _causal, _bh, _m, _n = _parse_fa_key(key)
+        for splits in ((1, 2) if variant == hip_lib.FA_VARIANT_SLICED else (1,)):
+            res = cfgs.fa_resources(variant, dtype, D, cfgs.FaTileChoice(*entry["tile"], splits))
+            assert res is not None, (key, splits)
+            assert res["scratch_bytes_per_lane"] == 0, (key, splits, res)
+    for key, entry in table["gemm"].items():
+        res = cfgs.gemm_resources(tuple(entry["tile"]))
+        assert res is not None and res["scratch_bytes_per_lane"] == 0, (key, res)
+
+
 def test_shapes_in_one_bucket_share_an_entry():
     k1 = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192)
     k2 = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 2, 64, 5000, 7000)
