@@ -49,14 +49,38 @@ FA_CONFIGS = {
     "bf16_d256": dict(B=2, H=16, N=8192, D=256, dtype="bf16", causal=False, variant="sliced", input_scale=0.5),
 }
 GEMM_SHAPE = dict(M=8192, N=8192, K=8192)
+GEMM_K256_SHAPE = dict(M=8192, N=8192, K=256)
 
 
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _time_launches(torch, fn, steps: int, warmup: int):
-    """Warm up, then time exactly `steps` launches; per-launch HIP events on the current stream."""
+def _clock_warmup(torch, fn, ms: float) -> int:
+    """Run `fn` back to back until at least `ms` of GPU time has passed (batches timed with HIP
+    events); returns the launch count. After the GPU has idled (host-side input setup), MI355X
+    takes ~30 ms of load to reach its steady clock: the 8192^3 GEMM measured 1030 TFLOP/s over its
+    first 5 launches, 1282 over launches 10-40 and 1345 from launch 40 on. The reference warms the
+    clock before timing too (torch.cuda._sleep, test_flash_atten.py:502-506)."""
+    done, n, spent = 0, 1, 0.0
+    while spent < ms:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        spent += s.elapsed_time(e)
+        done += n
+        n = min(2 * n, 64)
+    return done
+
+
+def _time_launches(torch, fn, steps: int, warmup: int, clock_warmup_ms: float = 0.0):
+    """Warm the clock (`clock_warmup_ms` of back-to-back launches), do `warmup` untimed launches,
+    then time exactly `steps` launches; per-launch HIP events on the current stream."""
+    if clock_warmup_ms > 0:
+        _clock_warmup(torch, fn, clock_warmup_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -386,6 +410,61 @@ def _counters_summarize(directory: str, fa_config: str, steps: int, fa_tile: str
     return 0
 
 
+def _bench_gemm_k256(torch, args, g, dev, vendor_rounds) -> dict:
+    """The reference's own GEMM test and chart shape (test_mma.py:42-45), 8192x8192x256, through the same
+    drop-in launcher: 128 MiB of C against 8 MiB of A and B, so its roofline is HBM (142.6 MB per launch,
+    17.8 us at 8 TB/s). Beside it: torch's fill of the same C (a pure 128 MiB write stream) and
+    hipBLASLt in alternating rounds."""
+    import mma
+
+    Mk, Nk, Kk = GEMM_K256_SHAPE["M"], GEMM_K256_SHAPE["N"], GEMM_K256_SHAPE["K"]
+    a = (torch.rand(Mk, Kk, generator=g) * 2 - 1).half().to(dev)
+    b = (torch.rand(Kk, Nk, generator=g) * 2 - 1).half().to(dev)
+    c = torch.empty(Mk, Nk, dtype=torch.float16, device=dev)
+    bm2, bn2, bk2, group_m2, warps2, stages2 = mma._select_2d_contiguous_config(Mk, Nk, Kk)
+    grid2 = (math.ceil(Mk / bm2) * math.ceil(Nk / bn2),)
+
+    def gemm_k256():
+        mma._matmul_contiguous_kernel[grid2](a, b, c, Mk, Nk, Kk, BLOCK_M=bm2, BLOCK_N=bn2, BLOCK_K=bk2,
+                                             GROUP_M=group_m2, USE_CACHE_EVICTION_HINTS=True, num_warps=warps2,
+                                             num_stages=stages2)
+
+    k_total, k_per = _time_launches(torch, gemm_k256, max(args.steps, 100), args.warmup, args.clock_warmup_ms)
+    k_steps = max(args.steps, 100)
+    k_ms = statistics.mean(k_per)
+    k_bytes = 2 * (Mk * Kk + Kk * Nk + Mk * Nk)
+    ref = a.float() @ b.float()
+    k_rel = ((c.float() - ref).norm() / ref.norm()).item()
+    del ref
+    fill_med = _alternating(torch, {"fill": lambda: c.fill_(1.0)}, rounds=3, per_round=20)["fill"]
+    k_vendor = None
+    if not args.no_vendor:
+        med = _alternating(torch, {"ours": gemm_k256, "hipblaslt": lambda: torch.matmul(a, b, out=c)},
+                           rounds=vendor_rounds[0], per_round=4 * vendor_rounds[1])
+        k_vendor = {"library": "torch.matmul (hipBLASLt)", "us": round(med["hipblaslt"] * 1e3, 2),
+                    "ours_same_rounds_us": round(med["ours"] * 1e3, 2),
+                    "speedup": round(med["hipblaslt"] / med["ours"], 3)}
+    gemm_k256_obj = {
+        "metric": "GEMM fp16 8192x8192x256 (the reference's test and chart shape)",
+        "us_per_step": round(k_total / k_steps * 1e3, 2),
+        "tflops": round(2.0 * Mk * Nk * Kk / (k_total / k_steps * 1e-3) / 1e12, 2),
+        "steps": k_steps,
+        "tile": {"block_m": bm2, "block_n": bn2, "block_k": bk2, "waves": warps2, "group_m": group_m2},
+        "rel_fro": k_rel,
+        "roofline": {"bound": "hbm", "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "kernel_us": round(k_ms * 1e3, 2), "algorithmic_bytes_per_launch": k_bytes,
+                     "algorithmic_flop_per_launch": 2.0 * Mk * Nk * Kk},
+        "c_fill_us": round(fill_med * 1e3, 2),
+        "vendor": k_vendor,
+    }
+    _log(f"gemm 8192x8192x256: {gemm_k256_obj['us_per_step']} us/step ({gemm_k256_obj['roofline']['frac']:.3f} of HBM "
+         f"peak), fill of C {gemm_k256_obj['c_fill_us']} us, vendor {k_vendor}")
+    del a, b, c
+    torch.cuda.empty_cache()
+    return gemm_k256_obj
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -402,6 +481,9 @@ def main() -> int:
                     help="attention tile as the reference's tune arguments (BLOCK_M, BLOCK_N, NUM_WARPS, "
                          "NUM_STAGES) instead of the tuning table's choice")
     ap.add_argument("--no-vendor", action="store_true", help="skip the alternating vendor-library timings")
+    ap.add_argument("--clock-warmup-ms", type=float, default=200.0,
+                    help="GPU time of back-to-back launches before each kernel's warm-up launches, so the timed "
+                         "launches run at the steady clock (0 disables)")
     ap.add_argument("--counter-run", action="store_true",
                     help="for rocprofv3 --pmc passes: calibration launches first, then 10 warm-up + 10 timed "
                          "launches of each kernel, no CPU or vendor legs")
@@ -469,7 +551,8 @@ def main() -> int:
     fa_flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
     _log(f"attention {args.fa_config} {variant}: tile {spec.kernel_kwargs['BLOCK_M']}x{spec.kernel_kwargs['BLOCK_N']} "
          f"waves={spec.kernel_kwargs['num_warps']} stages={spec.kernel_kwargs['num_stages']}")
-    total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup)
+    total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup,
+                                   args.clock_warmup_ms)
     fa_launch_ms = statistics.mean(per)
     fa_tflops_launch = fa_flops / (fa_launch_ms * 1e-3) / 1e12
     fa_ms_per_step = total_ms / args.steps
@@ -520,7 +603,7 @@ def main() -> int:
         mma._matmul_contiguous_kernel[grid](a, b, c, M, Ng, K, BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk, GROUP_M=group_m,
                                             USE_CACHE_EVICTION_HINTS=True, num_warps=warps, num_stages=stages)
 
-    g_total, g_per = _time_launches(torch, gemm, args.steps, args.warmup)
+    g_total, g_per = _time_launches(torch, gemm, args.steps, args.warmup, args.clock_warmup_ms)
     gemm_flops = 2.0 * M * Ng * K
     gemm_launch_ms = statistics.mean(g_per)
     gemm_tflops = gemm_flops / (g_total / args.steps * 1e-3) / 1e12
@@ -541,6 +624,12 @@ def main() -> int:
         _log(f"gemm vs hipBLASLt: {gemm_vendor}")
     del a, b, c
     torch.cuda.empty_cache()
+
+    # ---- GEMM at the reference's own test and chart shape (test_mma.py:42-45) ------------------------
+    # 8192x8192x256: 128 MiB of C against 8 MiB of A and B, so the roofline is HBM (142.6 MB per launch,
+    # 17.8 us at 8 TB/s); beside it, torch's fill of the same C (a pure 128 MiB write stream) on this GPU.
+    # (not in counter runs: their summaries take each kernel's last dispatches as the 8192^3 launches)
+    gemm_k256_obj = None if args.counter_run else _bench_gemm_k256(torch, args, g, dev, vendor_rounds)
 
     # ---- CPU baseline (reference CPU path, bounded sample) ---------------------------------------
     cpu_fa = cpu_gemm = None
@@ -611,6 +700,7 @@ def main() -> int:
             "cpu_baseline": cpu_gemm,
             "vendor": gemm_vendor,
         },
+        "gemm_k256": gemm_k256_obj,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -212,6 +212,22 @@ __device__ inline void wait_vm_lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The kernel's parameter struct read straight from the kernel-argument segment (scalar loads at
+// the point of use, instead of scalar registers held across a loop). Valid only for a kernel whose
+// one and only argument is a `P` passed by value: it then sits at offset 0 of the segment. Kernels
+// that call this pin their signature with kernel_has_sole_arg<P>(&kernel) (a compile-time check).
+template <typename P>
+__device__ inline const __attribute__((address_space(4))) P* kernarg_params() {
+  typedef const __attribute__((address_space(4))) P* Ptr;
+  Ptr ptr = (Ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(ptr));
+  return ptr;
+}
+template <typename P>
+constexpr bool kernel_has_sole_arg(void (*)(P)) { return true; }
+template <typename P, typename... Other>
+constexpr bool kernel_has_sole_arg(void (*)(Other...)) { return false; }
+
 // Workgroup id remapped so that consecutive logical ids land on the same XCD. Workgroups are
 // dispatched round-robin over the 8 XCDs of MI355X; logical id L = xcd * per + slot keeps
 // neighbouring tiles (which share K/V or A/B panels) inside one XCD's L2.

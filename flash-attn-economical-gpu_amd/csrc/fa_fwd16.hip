@@ -555,10 +555,9 @@ struct Fwd16 {
 
     // Epilogue: l over the four lane rows, O = acc / l; lane holds d = 16 dt + 4 g .. +3. The
     // output parameters are read again from the kernel-argument segment (scalar loads) rather than
-    // kept in scalar registers across the loop, where they would crowd out its own.
-    typedef const __attribute__((address_space(4))) FwdParams* KernargParams;
-    KernargParams pe = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(pe));
+    // kept in scalar registers across the loop, where they would crowd out its own; fa_fwd16_kernel
+    // takes FwdParams as its only argument (checked there), so the segment starts with it.
+    const auto pe = kernarg_params<FwdParams>();
     constexpr float kLn2 = 0.69314718055994530942f;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -598,6 +597,8 @@ struct Fwd16 {
 template <typename Tag, int D, int WAVES, int BN, int PIPE, bool SPLIT>
 __global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::kBlocksPerCu)) void fa_fwd16_kernel(
     FwdParams p) {
+  static_assert(kernel_has_sole_arg<FwdParams>(&fa_fwd16_kernel<Tag, D, WAVES, BN, PIPE, SPLIT>),
+                "run() reads FwdParams from kernel-argument offset 0: it must stay the only argument");
   Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run(p);
 }
 

@@ -154,8 +154,10 @@ int fa_fwd(const fa_fwd_args* args, void* stream);
  * args->workspace must be NULL and args->workspace_bytes 0. A launch whose partials
  * (fa_fwd_workspace_bytes) exceed the array fails with FA_EWORKSPACE before anything runs.
  * Calls on one GPU share its array: calls that overlap (other streams, other threads) race, so
- * the caller orders them. Launches without splits use no scratch and behave as fa_fwd. No
- * counterpart in the reference. */
+ * the caller orders them. Launches without splits use no scratch and behave as fa_fwd. The first
+ * call on a device looks up that device's array address (hipGetSymbolAddress), so make one call
+ * on each device before capturing fa_fwd_noalloc into a HIP graph. No counterpart in the reference
+ * (for callers that cannot allocate). */
 #define FA_NOALLOC_SCRATCH_BYTES (64LL << 20)
 int fa_fwd_noalloc(const fa_fwd_args* args, void* stream);
 

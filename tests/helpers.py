@@ -38,3 +38,19 @@ def rel_fro(actual, expected) -> float:
     actual = np.asarray(actual, dtype=np.float64)
     expected = np.asarray(expected, dtype=np.float64)
     return float(np.linalg.norm(actual - expected) / max(np.linalg.norm(expected), 1e-30))
+
+
+def oracle_rows_threaded(q, k, v, rows, *, causal: bool, scale: float | None = None, threads: int | None = None):
+    """oracle.attention_rows over `rows` (flattened (b*H + h)*M + m) split across host threads.
+
+    The C oracle runs without the GIL, so the chunks run in parallel; at most 16 threads (the GPU
+    box's CPU share)."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    rows = np.asarray(rows, dtype=np.int64)
+    n = threads or max(1, min(16, len(os.sched_getaffinity(0))))
+    chunks = [c for c in np.array_split(rows, n) if c.size]
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(lambda c: oracle.attention_rows(q, k, v, c, causal=causal, scale=scale), chunks))
+    return np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])

@@ -13,7 +13,7 @@ import hip_lib
 import mma
 import oracle
 from flash_atten import attention
-from helpers import ATOL
+from helpers import ATOL, oracle_rows_threaded
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -64,6 +64,82 @@ def test_config3_fa_fp16_b4h32d128(gpu, variant, causal, N):
     _check_rows(q, k, v, out, causal, B4H32_HEADS, rows_per_head=16, seed=N + int(causal))
     if causal:
         assert torch.equal(out[:, :, 0], v[:, :, 0])  # row 0 attends only key 0: O = V[0] exactly
+
+
+def _block_rows(B, H, M, block, seed):
+    """One flattened row (b*H + h)*M + m in every `block`-row query block of every (b, h), at a
+    random offset inside the block (so the rows land in every wave and lane position), plus the
+    last row of every (b, h)."""
+    rng = np.random.default_rng(seed)
+    nb = -(-M // block)
+    base = (np.arange(B * H, dtype=np.int64)[:, None] * M + np.arange(nb, dtype=np.int64)[None, :] * block)
+    m_in = np.minimum(rng.integers(0, block, size=base.shape), M - 1 - np.arange(nb)[None, :] * block)
+    last = np.arange(B * H, dtype=np.int64) * M + M - 1
+    return np.unique(np.concatenate([(base + m_in).ravel(), last]))
+
+
+# Tiles the config-3 workgroup sweep runs, besides the tuning table's choice: the ping-pong
+# 256-row kernel and the 128-row pipelined kernels (16x16 and 32x32 MFMA tiles).
+CONFIG3_TILES = [None, (256, 64, 8, 8), (128, 64, 4, 7), (128, 64, 4, 3)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_config3_every_workgroup(gpu, causal):
+    """BASELINE configs[2] at N = 8192 (the headline shape, and its causal case): one oracle row in
+    every 128-row query block of every (b, h) -- 8192 rows, so every workgroup of every tile's grid
+    (XCD remap, causal heaviest-first order, both ping-pong wave groups) is checked -- for the
+    table's tile and each listed tile, through the C ABI."""
+    B, H, N, D = 4, 32, 8192, 128
+    print(f"[fullsize] every workgroup fp16 4x32x8192x128 causal={causal}", flush=True)
+    q, k, v = (_randn((B, H, N, D), 40 + s + 10 * int(causal), torch.float16) for s in range(3))
+    rows = _block_rows(B, H, N, 128, seed=7 + int(causal))
+    assert rows.size >= B * H * (N // 128)
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    o_ref, lse_ref = oracle_rows_threaded(qn, kn, vn, rows, causal=causal)
+    del qn, kn, vn
+    rows_t = torch.from_numpy(rows).to(DEV)
+    for t in CONFIG3_TILES:
+        print(f"[fullsize]   tile {t or 'tuned'}", flush=True)
+        if t is None:
+            out, lse = attention(q, k, v, causal=causal, variant="optimized", return_lse=True)
+        else:
+            out = torch.empty_like(q)
+            lse = torch.empty((B, H, N), device=DEV, dtype=torch.float32)
+            hip_lib.fa_fwd(q, k, v, out, lse, sm_scale=D ** -0.5, causal=causal, variant=hip_lib.FA_VARIANT_OPT,
+                           tile=hip_lib.make_tile(*t, 1))
+        got = out.reshape(-1, D)[rows_t].float().cpu().numpy()
+        got_lse = lse.reshape(-1)[rows_t].cpu().numpy()
+        err = float(np.abs(got - o_ref).max())
+        err_lse = float(np.abs(got_lse - lse_ref).max())
+        print(f"[fullsize]   tile {t or 'tuned'}: max|dO| {err:.3e} max|dLSE| {err_lse:.3e}", flush=True)
+        assert err <= ATOL[torch.float16], (t, err)
+        assert err_lse <= 1e-3, (t, err_lse)
+        del out, lse
+
+
+# The reference's own pipeline cases at long sequence (test_flash_atten.py:82-88): B=1, H28 D128
+# and H16 D256, fp16, non-causal, S = 32768 and 65536; all three variants.
+@pytest.mark.parametrize("S", [32768, 65536])
+@pytest.mark.parametrize("H,D", [(28, 128), (16, 256)])
+def test_reference_long_sequence_cases(gpu, H, D, S):
+    print(f"[fullsize] reference pipeline case B1 H{H} D{D} S{S}", flush=True)
+    q, k, v = (_randn((1, H, S, D), 60 + s + S // 1024, torch.float16) for s in range(3))
+    rng = np.random.default_rng(S + D)
+    # per head: 8 random rows, the first and the last
+    rows = np.unique(np.concatenate([h * S + np.concatenate([[0, S - 1], rng.integers(0, S, 8)])
+                                     for h in range(H)]).astype(np.int64))
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    o_ref, _ = oracle_rows_threaded(qn, kn, vn, rows, causal=False)
+    del qn, kn, vn
+    rows_t = torch.from_numpy(rows).to(DEV)
+    for variant in ("basic", "optimized", "sliced"):
+        out = attention(q, k, v, causal=False, variant=variant)
+        got = out.reshape(-1, D)[rows_t].float().cpu().numpy()
+        assert torch.isfinite(out).all()
+        err = float(np.abs(got - o_ref).max())
+        print(f"[fullsize]   {variant}: max|dO| {err:.3e}", flush=True)
+        assert err <= ATOL[torch.float16], (variant, err)
+        del out
 
 
 @pytest.mark.parametrize("N", [1024, 2048, 4096, 8192])

@@ -75,6 +75,34 @@ def test_noalloc_without_splits_equals_fa_fwd(gpu):
     assert torch.equal(o_a, o_b) and torch.equal(lse_a, lse_b)
 
 
+def test_noalloc_replays_in_a_hip_graph(gpu):
+    """A split launch of fa_fwd_noalloc captured in a HIP graph: after one eager call (the first
+    call on a device resolves the scratch array's address, which the header requires outside
+    capture), the captured split pass + merge replay with new q/k/v contents written in place by
+    eager work between replays, and every replay equals an eager fa_fwd (torch workspace) on the
+    same inputs bit for bit."""
+    case = ("graph_split", 1, 8, 2, 64, 3000, 128, F16, False, 8, (128, 64, 4, 3))
+    name, B, H, Hkv, M, N, D, dtype, causal, splits, (bm, bn, waves, stages) = case
+    print(f"[no_alloc] graph capture B={B} H={H} Hkv={Hkv} M={M} N={N} D={D} splits={splits}", flush=True)
+    _, (qd, kd, vd) = _inputs(case)
+    _run(case, qd, kd, vd, noalloc=True)
+    o = torch.empty_like(qd)
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=qd.device)
+    kw = dict(sm_scale=D ** -0.5, causal=causal, variant=SLICED, tile=hip_lib.make_tile(bm, bn, waves, stages, splits))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hip_lib.fa_fwd_noalloc(qd, kd, vd, o, lse, **kw)
+    g = torch.Generator().manual_seed(11)
+    for rep in range(4):
+        for t in (qd, kd, vd):
+            t.copy_(torch.randn(t.shape, generator=g).to(dtype))
+        o_ref, lse_ref = _run(case, qd, kd, vd, noalloc=False)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref), rep
+        assert torch.equal(lse, lse_ref), rep
+
+
 def test_noalloc_rejects_oversized_partials_before_launch(gpu):
     B, H, M, N, D, splits = 4, 32, 2048, 4096, 128, 4
     need = hip_lib.workspace_bytes(B, H, M, D, splits)
