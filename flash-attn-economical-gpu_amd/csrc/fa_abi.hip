@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <atomic>
 #include <string>
 
 #include "fa_kernels.h"
@@ -44,7 +45,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 const fa::FaKernelEntry* find_fwd(int stages, int dtype, int D, int waves, int rows_per_wave, int block_n,
                                   int split) {
-  // stages 1-5: fa_fwd.hip (32x32x16 MFMAs); stages 6-7: fa_fwd16.hip (16x16x32 MFMAs)
+  // stages 1-5: fa_fwd.hip (32x32x16 MFMAs); stages 6-9: fa_fwd16.hip (16x16x32 MFMAs)
   int n = 0;
   const fa::FaKernelEntry* e = stages >= 6 ? fa::fa_fwd16_registry(&n) : fa::fa_fwd_registry(&n);
   for (int i = 0; i < n; ++i)
@@ -73,11 +74,33 @@ const fa::GemmKernelEntry* find_gemm(const gemm_tile* t) {
 }
 
 // Pipeline of a launch: basic keeps one K/V buffer (1); optimized and sliced double-buffer K/V (2),
-// or, when the tile asks for stages 3-8, run that LDS-DMA kernel (3-5: 32x32x16 MFMA tiles, 6-8:
+// or, when the tile asks for stages 3-9, run that LDS-DMA kernel (3-5: 32x32x16 MFMA tiles, 6-9:
 // 16x16x32 ones; the stages doc of fa_tile in the header lists them).
 int stages_of(int variant, const fa_tile* t) {
   if (variant == FA_VARIANT_BASIC) return 1;
-  return (t != nullptr && t->stages >= 3 && t->stages <= 8) ? t->stages : 2;
+  return (t != nullptr && t->stages >= 3 && t->stages <= 9) ? t->stages : 2;
+}
+
+// Compute units of the current device (the persistent kernel's grid), looked up once per device.
+int current_device_cus(int* cus) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(FA_EHIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int known = cache[dev].load(std::memory_order_relaxed);
+    if (known > 0) {
+      *cus = known;
+      return FA_OK;
+    }
+  }
+  int n = 0;
+  err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess || n <= 0) return fail(FA_EHIP, "hipDeviceGetAttribute(CU count) failed: %s", hipGetErrorString(err));
+  if (dev >= 0 && dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
+  *cus = n;
+  return FA_OK;
 }
 
 // Resolve (variant, tile) to the main kernel; nullptr + message when not built.
@@ -252,6 +275,12 @@ static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* st
   // them instead of once per query head.
   const int group = a->H / a->H_kv;
   const int pack = fa_fwd_pack_group(a->H, a->H_kv, a->M, a->causal, bm, splits);
+  if (e->stages == 9 && (pack > 1 || (int64_t)a->M * a->q_stride[2] * 2 > 0xffffffffLL || a->q_stride[2] < a->D)) {
+    // The persistent kernel fetches Q rows of one (batch, head) by LDS-DMA (32-bit offsets, whole
+    // rows) and does not pack query heads: the per-workgroup ping-pong kernel runs these launches.
+    e = find_fwd(8, e->dtype, e->D, e->waves, e->rows_per_wave, e->block_n, e->split);
+    if (e == nullptr) return fail(FA_ENOTSUP, "no stages=8 kernel behind the persistent attention tile");
+  }
   const int64_t m_blocks = ((int64_t)a->M * pack + bm - 1) / bm;
   const int64_t n_tiles = a->N > 0 ? (a->N + bn - 1) / bn : 1;
   const int64_t tiles_per_split = (n_tiles + splits - 1) / splits;
@@ -297,7 +326,15 @@ static int launch_fwd(const fa_fwd_args* a, void* ws, int64_t ws_bytes, void* st
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* kargs[] = {&p};
-  hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0, s);
+  int64_t grid = total;
+  if (e->stages == 9) {  // persistent: one workgroup per CU (fewer when there are fewer blocks)
+    int cus = 0;
+    const int code = current_device_cus(&cus);
+    if (code != FA_OK) return code;
+    if (grid > cus) grid = cus;
+  }
+  p.grid = (int32_t)grid;
+  hipError_t err = hipLaunchKernel(e->fn, dim3((unsigned)grid), dim3(e->waves * 64), kargs, 0, s);
   if (err != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(err));
 
   if (split) {

@@ -60,8 +60,11 @@ struct Fwd16 {
   // Workgroups per CU the launch bounds ask for: the one-tile-per-step kernel with 32-key tiles at
   // D <= 128 fits three (LDS and registers), the others two (the pipelined kernel holds two score
   // tiles).
-  static constexpr int kBlocksPerCu = PIPE == 2 ? 1 : (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
-  static_assert(PIPE != 2 || WAVES == 8, "the ping-pong kernel runs two groups of four waves");
+  static constexpr int kBlocksPerCu = PIPE >= 2 ? 1 : (!PIPE && BN == 32 && D <= 128) ? 3 : 2;
+  static_assert(PIPE < 2 || WAVES == 8, "the ping-pong kernels run two groups of four waves");
+  // Q fragments of the workgroup's rows in LDS (persistent kernel): block (wave, qt, cc) of 1 KiB
+  // holds, at byte 16 l, Q[row wave*ROWS + 16 qt + (l & 15)][32 cc + 8 (l >> 4) .. +7] -- lane l's qf.
+  static constexpr int QB_ELEMS = PIPE == 3 ? WAVES * QT * DC * 512 : 0;
   static constexpr bool kScalarIds = BN == 64 && PIPE != 1;
 
   typedef DT<Tag> T;
@@ -278,6 +281,314 @@ struct Fwd16 {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 2);
     }
+  }
+
+  // Epilogue of one work item of the persistent kernel (the same code as the end of run(), which
+  // keeps its copy inline: called there, even always-inlined, it pushed the 32-key one-tile-per-step
+  // kernel past its 168-VGPR cap into scratch). l over the four lane rows, O = acc / l; lane holds
+  // d = 16 dt + 4 g .. +3. The output parameters are read from the kernel-argument segment (scalar
+  // loads at the point of use); fa_fwd16_kernel takes FwdParams as its only argument (checked there).
+  __device__ __attribute__((always_inline)) static inline void store_out(const OAcc& acc, const float (&m_use)[QT], const float (&l_i)[QT],
+                                          const floatx4 (&lsum)[QT], int wrow0, int q16, int g, int rows, int b, int h,
+                                          int split_u) {
+    const auto pe = kernarg_params<FwdParams>();
+    constexpr float kLn2 = 0.69314718055994530942f;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float l = kSumMfma ? lsum[qt][0] : xquad_sum(l_i[qt]);
+      const int i = wrow0 + qt * 16 + q16;
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      if (i < rows) {
+        const int hr = pe->pack > 1 ? h + i / pe->M : h;
+        const int mr = pe->pack > 1 ? i % pe->M : i;
+        if (SPLIT) {
+          const int64_t wrow = (int64_t)(split_u * pe->B + b) * pe->H + hr;  // [split][b][h][m] rows
+          float* wo = pe->ws_o + (wrow * pe->M + mr) * D;
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            floatx4 val = {acc[dt][qt][0] * inv, acc[dt][qt][1] * inv, acc[dt][qt][2] * inv, acc[dt][qt][3] * inv};
+            *reinterpret_cast<floatx4*>(wo + dt * 16 + 4 * g) = val;
+          }
+          if (g == 0) pe->ws_lse[wrow * pe->M + mr] = lse_val;
+        } else {
+          uint16_t* orow = pe->o + (int64_t)b * pe->so0 + (int64_t)hr * pe->so1 + (int64_t)mr * pe->so2;
+#pragma unroll
+          for (int dt = 0; dt < DTL; ++dt) {
+            u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
+                         T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+          }
+          float* lse = pe->lse;
+          if (lse != nullptr && g == 0)
+            lse[(int64_t)b * pe->sl0 + (int64_t)hr * pe->sl1 + (int64_t)mr * pe->sl2] = lse_val;
+        }
+      }
+    }
+  }
+
+  // ---- persistent ping-pong (stages=9) ----------------------------------------------------------
+  // One workgroup per CU walks a fixed sequence of work items (the logical blocks of run()). The
+  // sequence is a snake over the XCD's slots: item k of XCD x goes to slot k % S in round k / S,
+  // slots reversed in odd rounds, so that with heaviest-first causal blocks each slot's rounds pair
+  // a heavy block with a light one. Within an item the schedule is run()'s ping-pong; across items
+  // the K/V rings keep running: the last two steps of an item fetch the next item's K_0, K_1 and
+  // V_0 into the slots the ring frees, and its first step fetches the next item's Q into an LDS
+  // buffer (each wave's own fragments), so an item starts without waiting on memory.
+  // A work item: its logical block (decoded to batch, head and split where needed: few scalar
+  // registers stay live across the KV loop), first query row and KV tile range.
+  struct Item {
+    int pid, m0, t_begin, ntiles;
+  };
+  struct Ids {
+    int b, h, hk, split;
+  };
+  template <class P>
+  __device__ static inline Ids decode(int pid, const P& p) {
+    const int rest = pid / p.m_blocks;
+    const int bh = rest / p.splits;
+    Ids ids;
+    ids.split = __builtin_amdgcn_readfirstlane(rest % p.splits);
+    ids.b = __builtin_amdgcn_readfirstlane(bh / p.H);
+    ids.h = __builtin_amdgcn_readfirstlane(bh % p.H);
+    ids.hk = __builtin_amdgcn_readfirstlane(ids.h / p.group);
+    return ids;
+  }
+  // Buffer descriptors of an item's K and V rows (its (batch, kv head)) and Q rows (batch, head).
+  template <class P>
+  __device__ static inline u32x4 k_rsrc(const Ids& d, const P& p) {
+    return make_rsrc(p.k + (int64_t)d.b * p.sk0 + (int64_t)d.hk * p.sk1, (uint32_t)p.N * (uint32_t)p.sk2 * 2u);
+  }
+  template <class P>
+  __device__ static inline u32x4 v_rsrc(const Ids& d, const P& p) {
+    return make_rsrc(p.v + (int64_t)d.b * p.sv0 + (int64_t)d.hk * p.sv1, (uint32_t)p.N * (uint32_t)p.sv2 * 2u);
+  }
+  template <class P>
+  __device__ static inline u32x4 q_rsrc(const Ids& d, const P& p) {
+    return make_rsrc(p.q + (int64_t)d.b * p.sq0 + (int64_t)d.h * p.sq1, (uint32_t)p.M * (uint32_t)p.sq2 * 2u);
+  }
+  // Logical block of round r for workgroup w of G, or -1 past the end of its sequence.
+  __device__ static inline int item_pid(int r, int w, int G, int total) {
+    int x = 0, slot = w, S = G, per = total;
+    if ((total & 7) == 0 && (G & 7) == 0) {  // XCD x = w % 8 walks logical blocks [x per, (x+1) per)
+      x = w & 7;
+      slot = w >> 3;
+      S = G >> 3;
+      per = total >> 3;
+    }
+    const int k = r * S + ((r & 1) ? S - 1 - slot : slot);
+    return k < per ? x * per + k : -1;
+  }
+  template <class P>
+  __device__ static inline Item make_item(int pid, const P& p) {
+    Item it;
+    it.pid = pid;
+    int mb = pid % p.m_blocks;
+    if (p.causal) mb = p.m_blocks - 1 - mb;  // heaviest query blocks first, as run()
+    it.m0 = __builtin_amdgcn_readfirstlane(mb) * BM;
+    const int split = (pid / p.m_blocks) % p.splits;
+    it.t_begin = __builtin_amdgcn_readfirstlane(split * p.tiles_per_split);
+    int n_end = (it.t_begin + p.tiles_per_split) * BN;
+    if (n_end > p.N) n_end = p.N;
+    if (p.causal && n_end > it.m0 + BM) n_end = it.m0 + BM;
+    const int t_end = (n_end + BN - 1) / BN;
+    it.ntiles = __builtin_amdgcn_readfirstlane(t_end > it.t_begin ? t_end - it.t_begin : 0);
+    return it;
+  }
+
+  template <int GRP>
+  __device__ static void persistent_group(const FwdParams& p, uint16_t* smem, int lane, int wave, int first_pid) {
+    // lane-derived values are computed inside each group's copy of the loop: shared ones, hoisted
+    // above the group branch, stayed live across group 0's loop and spilled
+    asm volatile("" : "+v"(lane));
+    const int q16 = lane & 15, g = lane >> 4;
+    // workgroup id and count from the builtin and the host (blockIdx / gridDim go through library
+    // calls that this build does not inline, whose results the compiler cannot prove uniform)
+    const int G = p.grid, w = (int)__builtin_amdgcn_workgroup_id_x();
+    // per-lane DMA offsets (item-independent): K, V as run(); Q rows of this wave within an item
+    uint32_t koff, voff;
+    {
+      const int blk = wave * NKW, jt = blk / DC, cc = blk % DC;
+      const uint32_t row = jt * 16 + (lane & 15), c0 = cc * 32 + 8 * (lane >> 4);
+      koff = (row * (uint32_t)p.sk2 + c0) * 2u;
+    }
+    {
+      const int blk = wave * NVW, kc = blk / DTL, dt = blk % DTL;
+      const int m = lane;
+      const uint32_t row = kc * 32 + 16 * (m >> 5) + 4 * ((m & 31) >> 3) + ((m & 7) >> 1);
+      const uint32_t c0 = dt * 16 + 8 * (m & 1);
+      voff = (row * (uint32_t)p.sv2 + c0) * 2u;
+    }
+    uint32_t qoff[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+      qoff[qt] = ((uint32_t)(wave * ROWS + qt * 16 + q16) * (uint32_t)p.sq2 + 8 * g) * 2u;
+    uint16_t* kring = smem;
+    uint16_t* vring = smem + 2 * KT_ELEMS;
+    const uint16_t* qbuf = smem + 2 * (KT_ELEMS + VT_ELEMS);
+    const uint32_t kring_lds = lds_address(smem), vring_lds = kring_lds + 2 * KT_ELEMS * 2;
+    const uint32_t qbuf_lds = kring_lds + 2 * (KT_ELEMS + VT_ELEMS) * 2;
+    const uint16_t* klane = kring + lane * 8;
+    const uint16_t* vlane = vring + lane * 4;
+    const uint16_t* qlane = qbuf + (wave * QT * DC) * 512 + lane * 8;
+
+    // bytes between consecutive KV tiles of K and of V (the host keeps them below 2^32)
+    const uint32_t kstep = (uint32_t)BN * (uint32_t)p.sk2 * 2u, vstep = (uint32_t)BN * (uint32_t)p.sv2 * 2u;
+    // Item-level parameters (pointers, strides, grid shape) are read through a fresh kernel-
+    // argument pointer at each item boundary rather than held in scalar registers across the KV
+    // loop: held there, they pushed the loop's own scalars out, and the compiler re-read strides
+    // with scalar loads inside the loop, whose waits (lgkmcnt, shared with LDS reads) then
+    // serialised every LDS fragment read.
+    Item cur = make_item(first_pid, *kernarg_params<FwdParams>());
+    int par = 0;              // ring slot of the current item's tile 0
+    bool prefetched = false;  // its Q, K_0, K_1, V_0 were fetched by the previous item
+    for (int r = 0;; ++r) {
+      const auto pi = kernarg_params<FwdParams>();
+      const int pid_n = item_pid(r + 1, w, pi->grid, pi->total_blocks);
+      Item nxt;
+      if (pid_n >= 0) {
+        nxt = make_item(pid_n, *pi);
+      } else {
+        nxt = cur;
+        nxt.ntiles = 0;
+      }
+      const int ntiles = cur.ntiles;
+      const u32x4 krs = k_rsrc(decode(cur.pid, *pi), *pi), vrs = v_rsrc(decode(cur.pid, *pi), *pi);
+      const int wrow0 = cur.m0 + wave * ROWS;
+      const bool wave_has_rows = wrow0 < p.M;
+      // Tile u of the current item, or tile u - ntiles of the next one (K up to the next item's
+      // tile 1, V up to its tile 0), into ring slot (par + u) & 1.
+      // (The next item's branch builds its descriptors there, in the two steps per item that take
+      // it; the empty asm keeps the compiler from merging the two branches' loads into one, which
+      // would build those descriptors on every step.)
+      auto issue_k = [&](int u) {
+        const uint32_t slot = kring_lds + (uint32_t)((par + u) & 1) * (KT_ELEMS * 2) + wave * NKW * 1024;
+        if (__builtin_expect(u < ntiles, 1)) {
+          buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + (uint32_t)(cur.t_begin + u) * kstep, slot);
+        } else if (u - ntiles < nxt.ntiles) {
+          asm volatile("");
+          const uint32_t toff = (uint32_t)(nxt.t_begin + u - ntiles) * kstep;
+          const auto pn = kernarg_params<FwdParams>();
+          buffer_load16_to_lds_blocks<NKW, 64>(k_rsrc(decode(nxt.pid, *pn), *pn), koff + toff, slot);
+        }
+      };
+      auto issue_v = [&](int u) {
+        const uint32_t slot = vring_lds + (uint32_t)((par + u) & 1) * (VT_ELEMS * 2) + wave * NVW * 1024;
+        if (__builtin_expect(u < ntiles, 1)) {
+          buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + (uint32_t)(cur.t_begin + u) * vstep, slot);
+        } else if (u - ntiles < nxt.ntiles) {
+          asm volatile("");
+          const uint32_t toff = (uint32_t)(nxt.t_begin + u - ntiles) * vstep;
+          const auto pn = kernarg_params<FwdParams>();
+          buffer_load16_to_lds_blocks<NVW, 32>(v_rsrc(decode(nxt.pid, *pn), *pn), voff + toff, slot);
+        }
+      };
+      auto issue_q = [&](const Item& it) {
+        const auto pq = kernarg_params<FwdParams>();
+        const uint32_t moff = (uint32_t)it.m0 * (uint32_t)pq->sq2 * 2u;
+        const u32x4 qrs = q_rsrc(decode(it.pid, *pq), *pq);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          buffer_load16_to_lds_blocks<DC, 64>(qrs, qoff[qt] + moff, qbuf_lds + ((wave * QT + qt) * DC) * 1024);
+      };
+      auto kslot = [&](int u) { return klane + ((par + u) & 1) * KT_ELEMS; };
+      auto vslot = [&](int u) { return vlane + ((par + u) & 1) * VT_ELEMS; };
+
+      OAcc acc;
+      float m_use[QT], l_i[QT];
+      floatx4 lsum[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        m_use[qt] = FA_NEG_INF;
+        l_i[qt] = 0.f;
+        lsum[qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < DTL; ++dt) acc[dt][qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
+      }
+      if (ntiles > 0) {
+        // DMA over an item of T tiles: K 0..T+1 and V 0..T (tiles past T - 1 are the next item's).
+        // The previous item fetched this one's K_0, V_0 and, when T >= 2, K_1; with T == 1 this
+        // item's K_1 is the next item's K_0, fetched here.
+        if (!prefetched) {
+          issue_q(cur);
+          issue_k(0);
+          wait_vm_lds_barrier<0>();
+          issue_k(1);  // K_1 (or the next item's K_0) and V_0 land by the end of phase 2
+          issue_v(0);
+        } else if (ntiles == 1) {
+          issue_k(1);
+        }
+        u32x4 qf[QT][DC];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int cc = 0; cc < DC; ++cc) qf[qt][cc] = *reinterpret_cast<const u32x4*>(qlane + (qt * DC + cc) * 512);
+        STile s;
+        u32x4 pk[KC][QT];
+        auto mma_block = [&](int u) {  // S = Q K_{u+1}^T, O += P_u V_u
+          // in the last step the QK reads the slot holding the next item's K_0 (landed one step
+          // earlier; the step's DMA fills the other slot) and its S is never used: one
+          // straight-line block, as in run()
+          __builtin_amdgcn_s_setprio(1);
+          qk(s, qf, kslot(u + 1));
+          pv(acc, pk, vslot(u), lsum);
+          m_schedule<4>();
+          __builtin_amdgcn_s_setprio(0);
+        };
+        auto softmax_block = [&](int t) {
+          if (t < ntiles) softmax(s, pk, acc, m_use, l_i, lsum, (cur.t_begin + t) * BN, wrow0, q16, g, p);
+        };
+        if (GRP == 0 && wave_has_rows) {
+          qk(s, qf, kslot(0));
+          qk_schedule();
+        }
+        wait_vm_lds_barrier<63>();
+        if (wave_has_rows) {
+          if (GRP == 0) {
+            softmax_block(0);
+          } else {
+            qk(s, qf, kslot(0));
+            qk_schedule();
+          }
+        }
+        wait_vm_lds_barrier<0>();
+        for (int j = 1; j <= ntiles; ++j) {
+          issue_k(j + 1);
+          issue_v(j);
+          // every wave read its Q fragments before the barriers above: the buffer takes the next Q
+          if (j == 1 && nxt.ntiles > 0) issue_q(nxt);
+          if (wave_has_rows) {
+            if (GRP == 0) mma_block(j - 1);
+            else softmax_block(j - 1);
+          }
+          wait_vm_lds_barrier<63>();
+          if (wave_has_rows) {
+            if (GRP == 0) softmax_block(j);
+            else mma_block(j - 1);
+          }
+          wait_vm_lds_barrier<0>();
+        }
+      }
+      {
+        const auto pe = kernarg_params<FwdParams>();
+        const Ids ids = decode(cur.pid, *pe);
+        store_out(acc, m_use, l_i, lsum, wrow0, q16, g, pe->M, ids.b, ids.h, ids.split);
+      }
+      if (pid_n < 0) break;
+      prefetched = ntiles > 0 && nxt.ntiles > 0;
+      par = (par + ntiles) & 1;
+      cur = nxt;
+    }
+  }
+
+  __device__ static void run_persistent(const FwdParams& p) {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (KT_ELEMS + VT_ELEMS) + QB_ELEMS];
+    const int tid = (int)__builtin_amdgcn_workitem_id_x();
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pid0 = item_pid(0, (int)__builtin_amdgcn_workgroup_id_x(), p.grid, p.total_blocks);
+    if (pid0 < 0) return;  // workgroup-uniform: more workgroups than blocks
+    if (wave < 4) persistent_group<0>(p, smem, lane, wave, pid0);
+    else persistent_group<1>(p, smem, lane, wave, pid0);
   }
 
   __device__ static void run(const FwdParams& p) {
@@ -592,18 +903,22 @@ struct Fwd16 {
       }
     }
   }
+
 };
 
 template <typename Tag, int D, int WAVES, int BN, int PIPE, bool SPLIT>
 __global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::kBlocksPerCu)) void fa_fwd16_kernel(
     FwdParams p) {
   static_assert(kernel_has_sole_arg<FwdParams>(&fa_fwd16_kernel<Tag, D, WAVES, BN, PIPE, SPLIT>),
-                "run() reads FwdParams from kernel-argument offset 0: it must stay the only argument");
-  Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run(p);
+                "the epilogues read FwdParams from kernel-argument offset 0: it must stay the only argument");
+  if constexpr (PIPE == 3)
+    Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run_persistent(p);
+  else
+    Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>::run(p);
 }
 
-// Registry (stages=6: PIPE 0, stages=7: PIPE 1, stages=8: PIPE 2 with 8 waves; 32 query rows per
-// wave).
+// Registry (stages=6: PIPE 0, stages=7: PIPE 1, stages=8: PIPE 2 and stages=9: PIPE 3 with 8 waves;
+// 32 query rows per wave).
 #define FA16_SYM_TAG_f16_t "5f16_t"
 #define FA16_SYM_TAG_bf16_t "6bf16_t"
 #define FA16_SYMBOL(TAG, D, W, BN, PI, SP)                                                                    \
@@ -613,10 +928,10 @@ __global__ __launch_bounds__(WAVES * 64, (Fwd16<Tag, D, WAVES, BN, PIPE, SPLIT>:
   {6 + PI, DTYPE, D, W, 32, BN, SP, (const void*)&fa_fwd16_kernel<TAG, D, W, BN, PI, (SP != 0)>, \
    FA16_SYMBOL(TAG, D, W, BN, PI, SP)}
 #define FA16_PAIR(TAG, DTYPE, D, BN, PI) FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 0), FA16_ENTRY(TAG, DTYPE, D, 4, BN, PI, 1)
-#define FA16_PAIR8(TAG, DTYPE, D, BN) FA16_ENTRY(TAG, DTYPE, D, 8, BN, 2, 0), FA16_ENTRY(TAG, DTYPE, D, 8, BN, 2, 1)
+#define FA16_PAIR8(TAG, DTYPE, D, BN, PI) FA16_ENTRY(TAG, DTYPE, D, 8, BN, PI, 0), FA16_ENTRY(TAG, DTYPE, D, 8, BN, PI, 1)
 #define FA16_ENTRIES(TAG, DTYPE, D)                                                             \
   FA16_PAIR(TAG, DTYPE, D, 64, 0), FA16_PAIR(TAG, DTYPE, D, 32, 0), FA16_PAIR(TAG, DTYPE, D, 64, 1), \
-      FA16_PAIR(TAG, DTYPE, D, 32, 1), FA16_PAIR8(TAG, DTYPE, D, 64)
+      FA16_PAIR(TAG, DTYPE, D, 32, 1), FA16_PAIR8(TAG, DTYPE, D, 64, 2), FA16_PAIR8(TAG, DTYPE, D, 64, 3)
 
 static const FaKernelEntry kFwd16Entries[] = {
     FA16_ENTRIES(f16_t, FA_DTYPE_F16, 64),        FA16_ENTRIES(f16_t, FA_DTYPE_F16, 128),

@@ -44,8 +44,10 @@ VARIANT_BY_KERNEL = {
 #   6  stages 5 with 16x16x32 MFMA tiles,
 #   7  stages 3 with 16x16x32 MFMA tiles,
 #   8  ping-pong: 8 waves in two groups of four that alternate MFMA phases and softmax phases
-#      on the same SIMDs (16x16x32 MFMA tiles, 256 query rows per workgroup).
-# The basic variant uses stages 1; optimized and sliced use 2 to 8.
+#      on the same SIMDs (16x16x32 MFMA tiles, 256 query rows per workgroup),
+#   9  the ping-pong kernel in a persistent grid: one workgroup per CU walks a fixed sequence of
+#      query blocks and fetches the next block's Q, K and V during the current block's last steps.
+# The basic variant uses stages 1; optimized and sliced use 2 to 9.
 FA_TILE_SPACE = [
     (128, 64, 4, 3),
     (256, 64, 8, 3),
@@ -59,6 +61,7 @@ FA_TILE_SPACE = [
     (128, 64, 4, 7),
     (128, 32, 4, 7),
     (256, 64, 8, 8),
+    (256, 64, 8, 9),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),
@@ -76,8 +79,8 @@ FA_TILE_SPACE = [
 ]
 STAGES_BY_VARIANT = {
     hip_lib.FA_VARIANT_BASIC: (1,),
-    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 6, 7, 8, 2),
-    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 6, 7, 8, 2),
+    hip_lib.FA_VARIANT_OPT: (3, 4, 5, 6, 7, 8, 9, 2),
+    hip_lib.FA_VARIANT_SLICED: (3, 4, 5, 6, 7, 8, 9, 2),
 }
 
 # GEMM tiles in preference order: (block_m, block_n, block_k, waves).

@@ -62,8 +62,12 @@ enum { FA_VARIANT_BASIC = 0, FA_VARIANT_OPT = 1, FA_VARIANT_SLICED = 2 };
  *   7  the stages=3 pipeline with 16x16x32 MFMA tiles (D <= 128);
  *   8  ping-pong (block_m 256, 8 waves, block_n 64, D <= 128): two groups of four waves, one phase
  *      apart, alternate a matrix phase (QK^T of the next tile, PV of this one) and a softmax phase,
- *      so that on every SIMD one wave issues MFMAs while the other issues the exp/pack work.
- *   The LDS-DMA kernels (3-8) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
+ *      so that on every SIMD one wave issues MFMAs while the other issues the exp/pack work;
+ *   9  the stages=8 ping-pong in a persistent grid (one workgroup per CU walks a fixed sequence of
+ *      query blocks; the last steps of a block fetch the next block's Q, K and V, so blocks start
+ *      without waiting on memory). Launches whose query heads fa_fwd_pack_group would pack, or
+ *      whose Q rows (M * q_stride[2] * 2 bytes) reach 2^32, run the stages=8 kernel instead.
+ *   The LDS-DMA kernels (3-9) need (N + block_n) * max(k_stride[2], v_stride[2]) * 2 < 2^32
  *   bytes and row strides >= D; when a launch breaks either rule, fa_fwd runs the stages=2 kernel
  *   of the same block_m and waves instead (same block_n where built, else 64). fa_fwd_supported()
  *   reports such a tile as built only when that fallback is built too. */

@@ -42,6 +42,8 @@ TILES = {
     "m16p_128n32": (OPT, 128, 32, 4, 7),
     # ping-pong (stages=8): 8 waves in two groups one phase apart, 256 rows, 16x16x32 MFMAs
     "pp_256": (OPT, 256, 64, 8, 8),
+    # the ping-pong kernel in a persistent grid (stages=9): one workgroup per CU walks query blocks
+    "ppp_256": (OPT, 256, 64, 8, 9),
 }
 
 
@@ -142,11 +144,20 @@ CASES = [
     ("pp_ragged_causal", 1, 2, 1, 290, 290, 128, F16, True, "pp_256"),
     ("pp_idle_waves", 1, 2, 2, 40, 700, 128, F16, False, "pp_256"),  # waves 2-7 hold no rows
     ("pp_tiny", 1, 1, 1, 1, 1, 128, F16, False, "pp_256"),
+    ("ppp_d128", 1, 2, 2, 512, 512, 128, F16, False, "ppp_256"),
+    ("ppp_d128_bf16_causal", 1, 2, 2, 512, 512, 128, BF16, True, "ppp_256"),
+    ("ppp_d64", 2, 2, 2, 256, 448, 64, F16, False, "ppp_256"),
+    ("ppp_d64_bf16_causal", 1, 3, 3, 300, 576, 64, BF16, True, "ppp_256"),
+    ("ppp_gqa_causal", 1, 12, 2, 256, 256, 128, BF16, True, "ppp_256"),
+    ("ppp_ragged", 2, 3, 3, 200, 333, 128, F16, False, "ppp_256"),
+    ("ppp_ragged_causal", 1, 2, 1, 290, 290, 128, F16, True, "ppp_256"),
+    ("ppp_idle_waves", 1, 2, 2, 40, 700, 128, F16, False, "ppp_256"),
+    ("ppp_tiny", 1, 1, 1, 1, 1, 128, F16, False, "ppp_256"),
 ]
 
 
 @pytest.mark.parametrize("tile_name", ["pipe128", "pipe256", "pipe4_128", "pipe4_128n32", "lean128n32", "m16_128",
-                                       "m16_128n32", "m16p_128", "pp_256"])
+                                       "m16_128n32", "m16p_128", "pp_256", "ppp_256"])
 @pytest.mark.parametrize("n", [1, 64, 65, 128, 192, 256, 320, 384, 448, 512])
 def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     """1..8 KV tiles: the pipelined loops' prologues, unrolled pairs, peeled tails (stages=4: 1, 2
@@ -162,7 +173,7 @@ def test_fa_pipelined_tile_counts(gpu, tile_name, n):
     assert max_abs(lse, lse_ref) <= 1e-3
 
 
-@pytest.mark.parametrize("tile_name", ["opt256w8", "pipe128", "pipe256", "pp_256"])
+@pytest.mark.parametrize("tile_name", ["opt256w8", "pipe128", "pipe256", "pp_256", "ppp_256"])
 def test_fa_strided_bshd_layout(gpu, tile_name):
     """q/k/v/o as [B, S, H, D] memory viewed as [B, H, S, D] (row stride H*D): buffer ranges and
     DMA offsets of the pipelined kernel follow the strides."""
@@ -188,11 +199,49 @@ def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
     B, H, Hkv, M, N, D, dtype = 1, 4, 2, 256, 1000, 128, BF16
     print(f"[fa_abi] sliced pipelined splits={splits} causal={causal}", flush=True)
     q, k, v = make_qkv(78, B, H, Hkv, M, N, D, dtype)
-    for tile_name in ("pipe128", "pipe256", "pipe4_128", "m16_128", "m16p_128", "pp_256"):
+    for tile_name in ("pipe128", "pipe256", "pipe4_128", "m16_128", "m16p_128", "pp_256", "ppp_256"):
         o, lse = run_fa(q, k, v, variant=SLICED, tile=TILES[tile_name], causal=causal, dtype=dtype, splits=splits)
         o_ref, lse_ref = oracle.attention(q, k, v, causal=causal)
         assert max_abs(o, o_ref) <= ATOL[dtype], tile_name
         assert max_abs(lse, lse_ref) <= 1e-3, tile_name
+
+
+# Persistent grid (stages=9) with several work items per workgroup (more query blocks than CUs):
+# name, B, H, Hkv, M, N, D, dtype, causal, splits
+PERSISTENT_CASES = [
+    ("items_x2", 2, 32, 32, 2048, 2048, 128, F16, False, 1),
+    ("items_causal_snake", 2, 32, 32, 4096, 4096, 128, F16, True, 1),  # 4..64 tiles per item
+    ("items_one_tile", 4, 32, 32, 2048, 64, 128, F16, False, 1),       # T = 1: the next K_0 from the prologue
+    ("items_two_tiles", 4, 32, 32, 2048, 100, 128, BF16, False, 1),
+    ("items_three_tiles_d64", 2, 32, 32, 2048, 130, 64, F16, False, 1),
+    ("items_gqa_causal_ragged", 3, 24, 8, 1000, 777, 128, BF16, True, 1),
+    ("items_split_causal", 1, 32, 8, 2048, 2048, 128, BF16, True, 4),  # empty split items (causal)
+    ("items_not_multiple_of_8", 1, 37, 37, 1800, 300, 64, F16, False, 1),
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=[c[0] for c in PERSISTENT_CASES])
+def test_fa_persistent_items(gpu, case):
+    """stages=9 walks several query blocks per workgroup, fetching the next block's Q/K/V during the
+    current block's last steps; its per-block arithmetic is stages=8's, so outputs and LSE must be
+    bit-identical to the per-workgroup ping-pong kernel, and sampled rows match the oracle."""
+    name, B, H, Hkv, M, N, D, dtype, causal, splits = case
+    print(f"[fa_abi] persistent {name} B={B} H={H} Hkv={Hkv} M={M} N={N} D={D} {dtype} causal={causal} "
+          f"splits={splits}", flush=True)
+    q, k, v = make_qkv(4242 + M + N, B, H, Hkv, M, N, D, dtype)
+    variant = SLICED if splits > 1 else OPT
+    outs = {}
+    for stages in (8, 9):
+        outs[stages] = run_fa(q, k, v, variant=variant, tile=(variant, 256, 64, 8, stages), causal=causal,
+                              dtype=dtype, splits=splits)
+    o8, lse8 = outs[8]
+    o9, lse9 = outs[9]
+    assert np.array_equal(o9, o8), name
+    assert np.array_equal(lse9, lse8), name
+    rows = np.unique(np.random.default_rng(M + N).integers(0, B * H * M, 48))
+    o_ref, lse_ref = oracle.attention_rows(q, k, v, rows, causal=causal)
+    assert max_abs(o9.reshape(-1, D)[rows], o_ref) <= ATOL[dtype], name
+    assert max_abs(lse9.reshape(-1)[rows], lse_ref) <= 1e-3, name
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
