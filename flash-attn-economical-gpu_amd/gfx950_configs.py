@@ -31,7 +31,8 @@ VARIANT_BY_KERNEL = {
     "_flash_attn_fwd_kernel_block_d_nomask_contiguous": hip_lib.FA_VARIANT_SLICED,
 }
 
-# Attention tiles in preference order (used when the tuning table has no entry for a shape):
+# Attention tiles in preference order (used when the tuning table has no entry for a shape's variant,
+# dtype, head dim and causality; the first ones are the fastest measured at large sizes):
 # (block_m, block_n, waves, stages). stages selects the kernel pipeline:
 #   1  one K/V buffer, two barriers per KV tile (the basic variant),
 #   2  double-buffered K/V, one barrier per tile,
@@ -49,6 +50,10 @@ VARIANT_BY_KERNEL = {
 #      query blocks and fetches the next block's Q, K and V during the current block's last steps.
 # The basic variant uses stages 1; optimized and sliced use 2 to 9.
 FA_TILE_SPACE = [
+    (256, 64, 8, 8),
+    (128, 32, 4, 6),
+    (128, 64, 4, 7),
+    (256, 64, 8, 9),
     (128, 64, 4, 3),
     (256, 64, 8, 3),
     (128, 32, 4, 3),
@@ -57,11 +62,7 @@ FA_TILE_SPACE = [
     (128, 32, 4, 5),
     (128, 64, 4, 5),
     (128, 64, 4, 6),
-    (128, 32, 4, 6),
-    (128, 64, 4, 7),
     (128, 32, 4, 7),
-    (256, 64, 8, 8),
-    (256, 64, 8, 9),
     (256, 64, 8, 2),
     (256, 64, 4, 2),
     (128, 64, 4, 2),
@@ -227,10 +228,34 @@ def gemm_table_key(M: int, N: int, K: int) -> str:
     return f"M{_bucket(M)}|N{_bucket(N)}|K{_bucket(K)}"
 
 
+def _nearest_fa_entry(table: dict, key: str) -> dict | None:
+    """The entry for `key`, else the swept bucket of the same (variant, dtype, D, causal) nearest to
+    it: smallest sum of |log2| distances in B*H, M and N (ties: more work, then key order). Shapes
+    between the swept sizes (the reference's B=1 H=28 pipeline cases, say) then run the tile timed on
+    their neighbours instead of the fixed preference order."""
+    entry = table.get(key)
+    if entry is not None:
+        return entry
+    prefix, rest = key.rsplit("|", 3)[0], key.rsplit("|", 3)[1:]
+    want = [int(part.lstrip("BHMN")) for part in rest]
+    best, best_rank = None, None
+    for other, ent in sorted(table.items()):
+        o_prefix, o_rest = other.rsplit("|", 3)[0], other.rsplit("|", 3)[1:]
+        if o_prefix != prefix:
+            continue
+        have = [int(part.lstrip("BHMN")) for part in o_rest]
+        dist = sum(abs(math.log2(a) - math.log2(b)) for a, b in zip(want, have))
+        rank = (dist, -have[0] * have[1] * have[2])
+        if best_rank is None or rank < best_rank:
+            best, best_rank = ent, rank
+    return best
+
+
 def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M: int, N: int,
                    candidates: list[FaTileChoice]) -> FaTileChoice:
-    """Timed-table winner among candidates if recorded, else the first candidate (preference order)."""
-    entry = load_tune_table()["fa"].get(fa_table_key(variant, dtype, D, causal, B, H, M, N))
+    """Timed-table winner among candidates (the shape's bucket, else its nearest swept bucket of the
+    same variant, dtype, head dim and causality), else the first candidate (preference order)."""
+    entry = _nearest_fa_entry(load_tune_table()["fa"], fa_table_key(variant, dtype, D, causal, B, H, M, N))
     if entry is not None:
         want = tuple(entry["tile"])
         for c in candidates:

@@ -36,7 +36,8 @@ FA_SWEEP = (
     + [("bf16_d256", torch.bfloat16, 2, 16, 16, n, n, 256, False, ("basic", "optimized", "sliced"))
        for n in (1024, 2048, 4096, 8192)]
     + [("fp16_d64_cfg1", torch.float16, 1, 4, 4, 512, 512, 64, False, ("basic", "optimized", "sliced"))]
-    + [("ttft_bf16_gqa", torch.bfloat16, 1, 12, 2, n, n, 128, True, ("sliced", "optimized")) for n in (4096, 16384)]
+    + [(f"ttft_{name}_gqa", dt, 1, 12, 2, n, n, 128, True, ("sliced", "optimized"))
+       for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16)) for n in (4096, 16384, 65536)]
     + [("decode_bf16_gqa", torch.bfloat16, b, 32, 8, 1, n, 128, False, ("sliced",))
        for b, n in ((1, 8192), (1, 32768), (1, 131072), (8, 32768), (32, 8192))]
 )

@@ -117,6 +117,27 @@ def test_missing_table_falls_back_to_preference_order(tmp_path, monkeypatch, fre
     assert cfgs.choose_gemm_tile(8192, 8192, 8192) == (*cfgs.gemm_candidates()[0], cfgs.GEMM_DEFAULT_GROUP_M)
 
 
+def test_shape_without_bucket_takes_nearest_swept_bucket(tmp_path, monkeypatch, fresh_table_cache):
+    """A shape whose bucket was not swept (the reference's B=1 H=28 pipeline cases) runs the tile
+    of the nearest swept bucket of the same variant, dtype, head dim and causality; with no such
+    bucket it falls back to the preference order."""
+    opt, f16 = hip_lib.FA_VARIANT_OPT, torch.float16
+    near = cfgs.fa_table_key(opt, f16, 128, False, 4, 32, 8192, 8192)   # BH128 M8192 N8192
+    far = cfgs.fa_table_key(opt, f16, 128, False, 1, 4, 512, 512)       # BH4 M512 N512
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"fa": {near: {"tile": [128, 64, 4, 7]}, far: {"tile": [128, 64, 4, 5]}}, "gemm": {}}))
+    monkeypatch.setattr(cfgs, "TUNE_TABLE_PATH", path)
+    cands = cfgs.fa_candidates(opt, f16, 128)
+    got = cfgs.choose_fa_tile(opt, f16, 128, False, 1, 28, 8192, 8192, cands)   # BH32: 2 octaves from `near`
+    assert (got.block_m, got.block_n, got.waves, got.stages) == (128, 64, 4, 7)
+    got = cfgs.choose_fa_tile(opt, f16, 128, False, 1, 4, 700, 700, cands)      # next to `far`
+    assert (got.block_m, got.block_n, got.waves, got.stages) == (128, 64, 4, 5)
+    # causal (or another dtype / head dim) has no swept bucket here: preference order
+    assert cfgs.choose_fa_tile(opt, f16, 128, True, 1, 28, 8192, 8192, cands) == cands[0]
+    assert cfgs.choose_fa_tile(opt, torch.bfloat16, 128, False, 1, 28, 8192, 8192,
+                               cfgs.fa_candidates(opt, torch.bfloat16, 128)) == cfgs.fa_candidates(opt, torch.bfloat16, 128)[0]
+
+
 def test_table_entry_for_unbuilt_tile_is_ignored(tmp_path, monkeypatch, fresh_table_cache):
     key = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192)
     path = tmp_path / "t.json"
