@@ -532,7 +532,7 @@ struct Fwd16 {
           __builtin_amdgcn_s_setprio(1);
           qk(s, qf, kslot(u + 1));
           pv(acc, pk, vslot(u), lsum);
-          m_schedule<4>();
+          m_schedule<8>();
           __builtin_amdgcn_s_setprio(0);
         };
         auto softmax_block = [&](int t) {
@@ -729,7 +729,7 @@ struct Fwd16 {
         __builtin_amdgcn_s_setprio(1);
         qk(s, qf, klane + ((u + 1) & 1) * KT_ELEMS);
         pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
-        m_schedule<4>();
+        m_schedule<8>();
         __builtin_amdgcn_s_setprio(0);
       };
       auto softmax_block = [&](int t) {
