@@ -65,6 +65,10 @@ struct Fwd16 {
   // Q fragments of the workgroup's rows in LDS (persistent kernel): block (wave, qt, cc) of 1 KiB
   // holds, at byte 16 l, Q[row wave*ROWS + 16 qt + (l & 15)][32 cc + 8 (l >> 4) .. +7] -- lane l's qf.
   static constexpr int QB_ELEMS = PIPE == 3 ? WAVES * QT * DC * 512 : 0;
+  static constexpr int kQChunks = 4;  // steps over which the persistent kernel prefetches the next Q
+  // O leaves in 64-byte row pieces (pack_o_wide) except from the kernels held to three workgroups
+  // per CU, whose register cap the extra swap registers would exceed (they spilled).
+  static constexpr bool kWideO = !SPLIT && kBlocksPerCu < 3;
   static constexpr bool kScalarIds = BN == 64 && PIPE != 1;
 
   typedef DT<Tag> T;
@@ -299,6 +303,8 @@ struct Fwd16 {
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      u32x4 wide[DTL / 2];
+      if constexpr (kWideO) pack_o_wide(acc, qt, inv, wide);  // cross-lane: before the row test
       if (i < rows) {
         const int hr = pe->pack > 1 ? h + i / pe->M : h;
         const int mr = pe->pack > 1 ? i % pe->M : i;
@@ -313,11 +319,17 @@ struct Fwd16 {
           if (g == 0) pe->ws_lse[wrow * pe->M + mr] = lse_val;
         } else {
           uint16_t* orow = pe->o + (int64_t)b * pe->so0 + (int64_t)hr * pe->so1 + (int64_t)mr * pe->so2;
+          if constexpr (kWideO) {
 #pragma unroll
-          for (int dt = 0; dt < DTL; ++dt) {
-            u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
-                         T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
-            *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+            for (int pp = 0; pp < DTL / 2; ++pp)
+              *reinterpret_cast<u32x4*>(orow + 32 * pp + wide_col(g)) = wide[pp];
+          } else {
+#pragma unroll
+            for (int dt = 0; dt < DTL; ++dt) {
+              u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
+                           T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
+              *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+            }
           }
           float* lse = pe->lse;
           if (lse != nullptr && g == 0)
@@ -327,14 +339,39 @@ struct Fwd16 {
     }
   }
 
+  // O of query tile qt (times inv), rounded, as 16-byte lane chunks. The accumulator gives lane row g
+  // (lanes 16 g .. 16 g + 15) columns d = 16 dt + 4 g .. +3 of each d tile, so a store per tile
+  // writes 32 bytes of each of 16 rows, and every such half line is an L2 request of its own. One
+  // v_permlane16_swap per dword of tiles 2 pp and 2 pp + 1 (it swaps the odd 16-lane rows of one
+  // operand with the even rows of the other) leaves lane row g holding 8 consecutive columns of the
+  // pair, starting at 32 pp + wide_col(g): each store then writes 64 contiguous bytes of each row,
+  // half the store instructions and L2 requests. Cross-lane: call with every lane active.
+  __device__ static inline void pack_o_wide(const OAcc& acc, int qt, float inv, u32x4 (&wide)[DTL / 2]) {
+    static_assert(DTL % 2 == 0, "d tiles pair up");
+#pragma unroll
+    for (int pp = 0; pp < DTL / 2; ++pp) {
+      const floatx4& a = acc[2 * pp][qt];
+      const floatx4& b = acc[2 * pp + 1][qt];
+      const auto lo = __builtin_amdgcn_permlane16_swap(T::pack2(a[0] * inv, a[1] * inv), T::pack2(b[0] * inv, b[1] * inv),
+                                                       false, false);
+      const auto hi = __builtin_amdgcn_permlane16_swap(T::pack2(a[2] * inv, a[3] * inv), T::pack2(b[2] * inv, b[3] * inv),
+                                                       false, false);
+      wide[pp] = (u32x4){lo[0], hi[0], lo[1], hi[1]};
+    }
+  }
+  // First column, within a pair of d tiles, of lane row g's chunk: rows 0..3 hold tile 2 pp's
+  // columns 0..7, tile 2 pp + 1's 0..7, tile 2 pp's 8..15, tile 2 pp + 1's 8..15.
+  __device__ static inline int wide_col(int g) { return 8 * (((g & 1) << 1) | (g >> 1)); }
+
   // ---- persistent ping-pong (stages=9) ----------------------------------------------------------
   // One workgroup per CU walks a fixed sequence of work items (the logical blocks of run()). The
   // sequence is a snake over the XCD's slots: item k of XCD x goes to slot k % S in round k / S,
   // slots reversed in odd rounds, so that with heaviest-first causal blocks each slot's rounds pair
   // a heavy block with a light one. Within an item the schedule is run()'s ping-pong; across items
   // the K/V rings keep running: the last two steps of an item fetch the next item's K_0, K_1 and
-  // V_0 into the slots the ring frees, and its first step fetches the next item's Q into an LDS
-  // buffer (each wave's own fragments), so an item starts without waiting on memory.
+  // V_0 into the slots the ring frees, and its first steps fetch the next item's Q into an LDS
+  // buffer (each wave's own fragments, in kQChunks pieces), so an item starts without waiting on
+  // memory.
   // A work item: its logical block (decoded to batch, head and split where needed: few scalar
   // registers stay live across the KV loop), first query row and KV tile range.
   struct Item {
@@ -491,6 +528,22 @@ struct Fwd16 {
         for (int qt = 0; qt < QT; ++qt)
           buffer_load16_to_lds_blocks<DC, 64>(qrs, qoff[qt] + moff, qbuf_lds + ((wave * QT + qt) * DC) * 1024);
       };
+      // Chunk c (of kQChunks) of this wave's QT * DC Q blocks of item `it`. Every workgroup starts
+      // its items at about the same time, so the whole chip's next-item Q fetch issued in one step
+      // (64 KiB per workgroup) made that step wait on HBM; in chunks over the item's first steps
+      // it hides behind their K/V traffic (measured 1-4% faster; 8 chunks were slower than 4).
+      auto issue_q_chunk = [&](const Item& it, int c) {
+        const auto pq = kernarg_params<FwdParams>();
+        const uint32_t moff = (uint32_t)it.m0 * (uint32_t)pq->sq2 * 2u;
+        const u32x4 qrs = q_rsrc(decode(it.pid, *pq), *pq);
+#pragma unroll
+        for (int bq = 0; bq < QT * DC; ++bq) {
+          if (bq * kQChunks / (QT * DC) == c) {
+            const int qt = bq / DC, cc = bq % DC;
+            buffer_load16_to_lds(qrs, qoff[qt] + moff + cc * 64, qbuf_lds + ((wave * QT + qt) * DC + cc) * 1024);
+          }
+        }
+      };
       auto kslot = [&](int u) { return klane + ((par + u) & 1) * KT_ELEMS; };
       auto vslot = [&](int u) { return vlane + ((par + u) & 1) * VT_ELEMS; };
 
@@ -551,12 +604,22 @@ struct Fwd16 {
             qk_schedule();
           }
         }
-        wait_vm_lds_barrier<0>();
+        // A prefetched item's Q, K_0, K_1 and V_0 landed by the previous item's last wait; what is
+        // still in flight here is that item's O stores and (T == 1) the next item's K_0, which
+        // only step 1's discarded QK reads before step 1's own wait. So the barrier need not
+        // wait for memory (the O stores then drain during step 1).
+        if (prefetched) wait_vm_lds_barrier<63>();
+        else wait_vm_lds_barrier<0>();
         for (int j = 1; j <= ntiles; ++j) {
           issue_k(j + 1);
           issue_v(j);
-          // every wave read its Q fragments before the barriers above: the buffer takes the next Q
-          if (j == 1 && nxt.ntiles > 0) issue_q(nxt);
+          // every wave read its Q fragments before the barriers above: the buffer takes the next
+          // item's Q, chunk c at step min(c + 1, T), so all of it has landed by the item's last wait
+          if (nxt.ntiles > 0) {
+#pragma unroll
+            for (int c = 0; c < kQChunks; ++c)
+              if (j == min(c + 1, ntiles)) issue_q_chunk(nxt, c);
+          }
           if (wave_has_rows) {
             if (GRP == 0) mma_block(j - 1);
             else softmax_block(j - 1);
@@ -876,6 +939,8 @@ struct Fwd16 {
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      u32x4 wide[DTL / 2];
+      if constexpr (kWideO) pack_o_wide(acc, qt, inv, wide);  // cross-lane: before the row test
       if (i < rows) {
         const int hr = pe->pack > 1 ? h + i / pe->M : h;
         const int mr = pe->pack > 1 ? i % pe->M : i;
@@ -890,11 +955,17 @@ struct Fwd16 {
           if (g == 0) pe->ws_lse[wrow * pe->M + mr] = lse_val;
         } else {
           uint16_t* orow = pe->o + (int64_t)b * pe->so0 + (int64_t)hr * pe->so1 + (int64_t)mr * pe->so2;
+          if constexpr (kWideO) {
 #pragma unroll
-          for (int dt = 0; dt < DTL; ++dt) {
-            u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
-                         T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
-            *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+            for (int pp = 0; pp < DTL / 2; ++pp)
+              *reinterpret_cast<u32x4*>(orow + 32 * pp + wide_col(g)) = wide[pp];
+          } else {
+#pragma unroll
+            for (int dt = 0; dt < DTL; ++dt) {
+              u32x2 val = {T::pack2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
+                           T::pack2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv)};
+              *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = val;
+            }
           }
           float* lse = pe->lse;
           if (lse != nullptr && g == 0)
