@@ -5,7 +5,9 @@ Usage: python build_lib.py [--jobs N]
 Each csrc/*.hip file is compiled to an object in _build/ (in parallel), then linked into
 libfa_gfx950.so next to this file. The compiler's kernel-resource-usage remarks are parsed into
 kernel_resources.json (VGPR/AGPR/SGPR counts, LDS bytes, scratch, occupancy per kernel symbol), which
-the tuner's resource filter and the resource report read on hosts without a GPU.
+the tuner's resource filter and the resource report read on hosts without a GPU. Each file is also
+compiled to device assembly (_build/*.s) and checked for the gfx9 hazards the compiler leaves to
+hand-written asm (asm_hazards); a hit fails the build.
 """
 from __future__ import annotations
 
@@ -81,6 +83,76 @@ def _parse_resources(stderr: str) -> dict[str, dict[str, object]]:
     return kernels
 
 
+_SGPR_RE = re.compile(r"\bs\[(\d+):(\d+)\]|\bs(\d+)\b")
+
+
+def _sgprs(text: str) -> set[int]:
+    out: set[int] = set()
+    for m in _SGPR_RE.finditer(text):
+        if m.group(3) is not None:
+            out.add(int(m.group(3)))
+        else:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return out
+
+
+def _valu_sgpr_defs(instr: str) -> set[int]:
+    """SGPRs a vector-ALU instruction writes: the destination of v_readfirstlane / v_readlane, the
+    mask of a VOP3 compare, the carry-out of a VOP3 *_co_* add."""
+    op, _, rest = instr.partition(" ")
+    if not op.startswith("v_"):
+        return set()
+    operands = [o.strip() for o in rest.split(",")]
+    if op.startswith(("v_readfirstlane", "v_readlane")) or (op.startswith("v_cmp") and op.endswith("_e64")):
+        return _sgprs(operands[0]) if operands else set()
+    if "_co_" in op and op.endswith("_e64") and len(operands) > 1:
+        return _sgprs(operands[1])
+    return set()
+
+
+def asm_hazards(asm: str) -> list[str]:
+    """Hazards the compiler does not cover around the kernels' inline-asm memory instructions (gfx9):
+    a vector-memory instruction reading an SGPR within 5 wait states of a VALU write to it, and a
+    store of more than 8 bytes whose asm block does not end in an s_nop (a VALU write to its data
+    VGPRs needs 1 wait state after it)."""
+    lines = asm.splitlines()
+    found: list[str] = []
+    func = "?"
+    in_asm = False
+    for k, line in enumerate(lines):
+        t = line.strip()
+        if re.match(r"^_Z\w+:", line):
+            func = line.split(":")[0]
+        if t.startswith(";;#ASMSTART"):
+            in_asm, block_start = True, k
+            continue
+        if t.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        if not in_asm or not t.startswith(("buffer_load", "buffer_store")):
+            continue
+        op, _, rest = t.partition(" ")
+        if op.startswith("buffer_store") and op.endswith(("dwordx3", "dwordx4")):
+            nxt = next((lines[j].strip() for j in range(k + 1, len(lines)) if lines[j].strip()), "")
+            if not nxt.startswith("s_nop"):
+                found.append(f"{func}: asm {op} without a following s_nop")
+        used = _sgprs(rest)
+        waits, j = 0, k - 1
+        while j >= 0 and waits < 5:
+            u = lines[j].strip()
+            j -= 1
+            if not u or u.startswith((";", ".")):
+                continue
+            if u.startswith("s_nop"):
+                waits += int(u.split()[1], 0) + 1
+                continue
+            if _valu_sgpr_defs(u) & used:
+                found.append(f"{func}: '{u}' writes an SGPR that asm '{op}' reads {waits} wait states later")
+                break
+            waits += 1
+    return found
+
+
 def _compile(src: Path) -> tuple[Path, dict[str, dict[str, object]]]:
     obj = BUILD / (src.stem + ".o")
     cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
@@ -88,6 +160,17 @@ def _compile(src: Path) -> tuple[Path, dict[str, dict[str, object]]]:
     if proc.returncode != 0:
         sys.stderr.write(proc.stderr)
         raise RuntimeError(f"hipcc failed for {src.name} (exit {proc.returncode})")
+    # the same device code as assembly, checked for hazards around the inline-asm memory instructions
+    asm = BUILD / (src.stem + ".s")
+    flags = [f for f in HIPCC_FLAGS if not f.startswith("-Rpass")]
+    aproc = subprocess.run([_hipcc(), *flags, "--cuda-device-only", "-S", str(src), "-o", str(asm)],
+                           capture_output=True, text=True)
+    if aproc.returncode != 0:
+        sys.stderr.write(aproc.stderr)
+        raise RuntimeError(f"hipcc -S failed for {src.name} (exit {aproc.returncode})")
+    hazards = asm_hazards(asm.read_text())
+    if hazards:
+        raise RuntimeError(f"{src.name}: {len(hazards)} inline-asm hazard(s), first: {hazards[0]}")
     return obj, _parse_resources(proc.stderr)
 
 

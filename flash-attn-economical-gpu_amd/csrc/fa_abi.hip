@@ -428,12 +428,26 @@ int gemm_f16(const void* a, const void* b, void* c, int32_t M, int32_t N, int32_
   const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
   if (total > 0x7fffffffLL) return fail(FA_EINVAL, "grid too large");
   p.region_m = gemm_region_rows(p.tiles_m, p.tiles_n, e->block_m, e->block_n);
-  // Short K loops run the tile's shallow-ring kernel where one is built (more workgroups per CU).
+  // Short K loops run the tile's shallow-ring kernel where one is built (more workgroups per CU),
+  // or its persistent kernel (one workgroup per CU overlapping each tile's C write with the next
+  // tile) when the shape is whole tiles and C takes 16-byte stores.
   const int slabs = (K + e->block_k - 1) / e->block_k;
   const void* fn = (e->fn_shallow && slabs <= fa::kGemmShallowMaxSlabs) ? e->fn_shallow : e->fn;
+  unsigned grid = (unsigned)total, threads = (unsigned)e->waves * 64;
+  if (e->fn_persist && M % e->block_m == 0 && N % e->block_n == 0 && K % e->block_k == 0 &&
+      slabs >= fa::kGemmPersistMinSlabs && slabs <= fa::kGemmPersistMaxSlabs && total % 8 == 0 &&
+      aligned16(c) && ldc % 8 == 0 && (int64_t)e->block_m * ldc * 2 <= 0x7fffffffLL) {
+    int cus = 0;
+    if (current_device_cus(&cus) == FA_OK && cus >= 8) {
+      const int64_t g = (total < cus ? total : cus) / 8 * 8;  // whole XCD rows of workgroups
+      fn = e->fn_persist;
+      grid = (unsigned)g;
+      threads = (unsigned)(e->waves + fa::kGemmPersistStoreWaves) * 64;
+    }
+  }
+  p.grid = (int32_t)grid;
   void* kargs[] = {&p};
-  hipError_t err = hipLaunchKernel(fn, dim3((unsigned)total), dim3(e->waves * 64), kargs, 0,
-                                   static_cast<hipStream_t>(stream));
+  hipError_t err = hipLaunchKernel(fn, dim3(grid), dim3(threads), kargs, 0, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(FA_EHIP, "gemm launch failed: %s", hipGetErrorString(err));
   return ok();
 }

@@ -173,23 +173,35 @@ __device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
 // wave-uniform offset), so M0 is computed with scalar instructions. IMM is the instruction's 12-bit
 // offset field: the hardware adds it to the memory offset (byte_off) AND to the LDS address
 // (M0 + IMM + 16 * lane), so M0 is set to lds_block - IMM.
-template <int IMM = 0>
+// GUARD: 5 wait states before the load. On gfx9 a vector-memory instruction must not read an SGPR
+// (here the descriptor) within 5 wait states of a VALU write to it (v_readfirstlane, or v_readlane
+// restoring an SGPR the compiler spilled to a VGPR lane); the compiler inserts those for its own
+// memory instructions but cannot see into inline asm. Kernels whose build shows such a write
+// before this asm take the guard (build_lib.py checks every kernel's assembly for it).
+template <int IMM = 0, bool GUARD = false>
 __device__ inline void buffer_load16_to_lds(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
   static_assert(IMM >= 0 && IMM < 4096, "12-bit immediate offset");
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_block - (uint32_t)IMM);
-  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen offset:%3 lds"
-               :
-               : "v"(byte_off), "s"(lds), "s"(rsrc), "n"(IMM)
-               : "memory", "m0");
+  if constexpr (GUARD) {
+    asm volatile("s_nop 4\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen offset:%3 lds"
+                 :
+                 : "v"(byte_off), "s"(lds), "s"(rsrc), "n"(IMM)
+                 : "memory", "m0");
+  } else {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen offset:%3 lds"
+                 :
+                 : "v"(byte_off), "s"(lds), "s"(rsrc), "n"(IMM)
+                 : "memory", "m0");
+  }
 }
 
 // N consecutive 1 KiB blocks whose per-lane sources are STEP bytes apart: one offset register, the
 // steps in the immediate field.
-template <int N, int STEP, int J = 0>
+template <int N, int STEP, int J = 0, bool GUARD = false>
 __device__ inline void buffer_load16_to_lds_blocks(const u32x4& rsrc, uint32_t byte_off, uint32_t lds_block) {
   if constexpr (J < N) {
-    buffer_load16_to_lds<J * STEP>(rsrc, byte_off, lds_block + J * 1024u);
-    buffer_load16_to_lds_blocks<N, STEP, J + 1>(rsrc, byte_off, lds_block);
+    buffer_load16_to_lds<J * STEP, GUARD>(rsrc, byte_off, lds_block + J * 1024u);
+    buffer_load16_to_lds_blocks<N, STEP, J + 1, GUARD>(rsrc, byte_off, lds_block);
   }
 }
 

@@ -637,13 +637,13 @@ struct FwdKernel {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
         const uint32_t slot = kring_lds + (uint32_t)(u % RING) * (KT_ELEMS * 2);
-        buffer_load16_to_lds_blocks<NKW, 32>(krs, koff + toff, slot + wave * NKW * 1024);
+        buffer_load16_to_lds_blocks<NKW, 32, 0, true>(krs, koff + toff, slot + wave * NKW * 1024);
       };
       auto issue_v = [&](int u) {
         if (u >= ntiles) return;
         const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
         const uint32_t slot = vring_lds + (uint32_t)(u % RING) * (VT_ELEMS * 2);
-        buffer_load16_to_lds_blocks<NVW, 64>(vrs, voff + toff, slot + wave * NVW * 1024);
+        buffer_load16_to_lds_blocks<NVW, 64, 0, true>(vrs, voff + toff, slot + wave * NVW * 1024);
       };
       const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
       const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block

@@ -548,6 +548,237 @@ struct GemmKernel {
       }
     }
   }
+
+  // ---- persistent short-K kernel ----------------------------------------------------------------
+  // With a short K loop a tile's C write takes as long as its MFMAs, and a workgroup per tile
+  // issues the two in turn. Here one workgroup per CU walks its tiles (XCD x = w % 8 takes a
+  // contiguous range of the grouped tile order, its workgroups striding through it) in one
+  // continuous slab loop: the DMA for slabs past a tile's last fetches the next tile's first slabs,
+  // and the next tile's first chunk is read during the last chunk's MFMAs. A finished tile's C
+  // goes to LDS, and kGemmPersistStoreWaves more waves of the workgroup (one per SIMD) copy it to
+  // HBM during the next tile's first kStoreSteps slab steps. The store waves issue no loads and
+  // wait for nothing but the workgroup barriers, and the compute waves issue no stores, so their
+  // waits (vmcnt retires in order, loads and stores alike) see only their own slab DMA: C's write
+  // overlaps the next tile's loads and MFMAs instead of following them. (Stores issued by the
+  // compute waves after a step's DMA stalled the wait two steps later.)
+  // Shapes: whole tiles (M % BM, N % BN, K % BK zero), kGemmPersistMinSlabs.. K slabs, a grid that
+  // is a multiple of 8 and a tile count that is too (the host checks).
+  static constexpr int kStoreWaves = kGemmPersistStoreWaves;
+  // C rows leave after the barriers of slab steps 0 .. kStoreSteps - 1 of the next tile, so at
+  // least one barrier (step kStoreSteps <= ksteps - 1) separates the store waves' last LDS reads
+  // from the compute waves' next write of the tile after its last step.
+  static constexpr int kStoreSteps = 2;
+  static_assert(kStoreSteps + 1 <= kGemmPersistMinSlabs, "a barrier between the last C read and the next C write");
+  static constexpr int kHeldLds = BM * BN * 2;      // the C tile, row-major, 16-byte chunks swizzled
+  static constexpr int kRowChunks = BN / 8;         // 16-byte chunks per C row
+  static constexpr int kRowsPerStore = 64 / kRowChunks;  // rows one store-wave instruction writes
+  static constexpr int kStoreRows = BM / kStoreWaves / kStoreSteps;  // rows per store wave per step
+
+  // Byte offset of 16-byte chunk c of row r in the LDS C tile: chunks XORed with the row's low bits,
+  // so the 16 rows one compute-wave write touches, and the row one store-wave read touches, spread
+  // over all banks.
+  __device__ static inline int c_lds_off(int r, int c) { return r * (BN * 2) + ((c ^ (r & (kRowChunks - 1))) << 4); }
+
+  // The compute wave's C values, rounded, into the LDS tile. MFMA tile tn gives lane row g (lanes
+  // 16 g .. 16 g + 15) columns 4 g .. 4 g + 3; one v_permlane16_swap per dword of tiles 2 pp and
+  // 2 pp + 1 (it swaps the odd 16-lane rows of one operand with the even rows of the other) leaves
+  // lane row g holding columns 32 pp + 8 ((g & 1) << 1 | g >> 1) .. +7 of the pair: 16 bytes per
+  // lane. Cross-lane: all lanes active.
+  __device__ static inline void c_to_lds(const AccTiles& acc, char* ctile, int wm, int wn, int lane) {
+    const int r16 = lane & 15, g = lane >> 4;
+    const int cw = 8 * (((g & 1) << 1) | (g >> 1));
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int pp = 0; pp < TN / 2; ++pp) {
+        const auto lo = __builtin_amdgcn_permlane16_swap(
+            DT<f16_t>::pack2(acc_at(acc, 2 * pp, tm, 0), acc_at(acc, 2 * pp, tm, 1)),
+            DT<f16_t>::pack2(acc_at(acc, 2 * pp + 1, tm, 0), acc_at(acc, 2 * pp + 1, tm, 1)), false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap(
+            DT<f16_t>::pack2(acc_at(acc, 2 * pp, tm, 2), acc_at(acc, 2 * pp, tm, 3)),
+            DT<f16_t>::pack2(acc_at(acc, 2 * pp + 1, tm, 2), acc_at(acc, 2 * pp + 1, tm, 3)), false, false);
+        const int r = (wm * TM + tm) * MI + r16;
+        const int col = wn * (BN / WN) + 32 * pp + cw;
+        *reinterpret_cast<u32x4*>(ctile + c_lds_off(r, col / 8)) = (u32x4){lo[0], hi[0], lo[1], hi[1]};
+      }
+  }
+  // Rows r0 .. r0 + kStoreRows - 1 of the LDS C tile to C (`rsrc` over the tile's rows): each
+  // instruction writes kRowsPerStore whole tile rows, 16 bytes per lane.
+  __device__ static inline void c_rows_out(const char* ctile, const u32x4& rsrc, uint32_t ldc, int r0, int lane) {
+    const int rr = lane / kRowChunks, c = lane % kRowChunks;
+#pragma unroll
+    for (int q = 0; q < kStoreRows / kRowsPerStore; ++q) {
+      const int r = r0 + q * kRowsPerStore + rr;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ctile + c_lds_off(r, c));
+      const uint32_t off = ((uint32_t)r * ldc + (uint32_t)(c * 8)) * 2u;
+      // The s_nop covers the gfx9 hazard of a VALU write to the data VGPRs of a just-issued store of
+      // more than 8 bytes (one wait state), which the compiler does not see through inline asm.
+      asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" : : "v"(v), "v"(off), "s"(rsrc) : "memory");
+    }
+  }
+
+  __device__ static void run_persistent(const GemmParams& p) {
+    static_assert(MI == 16 && SCHED == 1 && TN % 2 == 0 && KCH % 2 == 0, "persistent kernel: pipelined 16x16 tiles");
+    static_assert(RING == 2, "persistent kernel waits assume a 2-slab ring");
+    static_assert(64 % kRowChunks == 0 && BM % (kStoreWaves * kStoreSteps * kRowsPerStore) == 0, "C rows split evenly");
+    static_assert(RING * SLAB_BYTES + kHeldLds <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(16))) char smem[RING * SLAB_BYTES + kHeldLds];
+    char* const ctile = smem + RING * SLAB_BYTES;
+    const int tid = (int)__builtin_amdgcn_workitem_id_x();
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // This workgroup's tiles: i-th is entry slot + i * S of XCD x's range of the grouped order.
+    const int G = p.grid, w = (int)__builtin_amdgcn_workgroup_id_x();
+    const int per = (p.tiles_m * p.tiles_n) / 8, S = G / 8, x = w % 8, slot = w / 8;
+    const int n_my = slot < per ? (per - 1 - slot) / S + 1 : 0;
+    if (n_my == 0) return;  // workgroup-uniform
+    auto tile_origin = [&](int i, int& m0, int& n0) {
+      const int pid = x * per + slot + i * S;
+      const int in_group = p.group_m * p.tiles_n;
+      const int first_m = (pid / in_group) * p.group_m;
+      const int gsz = min(p.tiles_m - first_m, p.group_m);
+      m0 = (first_m + (pid % in_group) % gsz) * BM;
+      n0 = ((pid % in_group) / gsz) * BN;
+    };
+    auto c_rsrc = [&](int m0, int n0) {
+      return make_rsrc(p.c + (int64_t)m0 * p.ldc + n0, (uint32_t)BM * (uint32_t)p.ldc * 2u);
+    };
+    const int ksteps = p.K / BK;
+
+    if (wave >= WAVES) {
+      // Store wave: the same barriers as the compute waves (one before the first tile, one per
+      // slab step, one after the last tile). After the barrier of step ks < kStoreSteps of tile
+      // i >= 1 it writes its rows of tile i - 1's C, which the compute waves put in LDS after tile
+      // i - 1's last barrier and overwrite only after tile i's last one; after the final barrier,
+      // its rows of the last tile.
+      const int r_base = (wave - WAVES) * (BM / kStoreWaves);
+      __builtin_amdgcn_s_barrier();
+      int pm0 = 0, pn0 = 0;
+      for (int i = 0; i < n_my; ++i) {
+        for (int ks = 0; ks < ksteps; ++ks) {
+          __builtin_amdgcn_s_barrier();
+          if (i > 0 && ks < kStoreSteps) c_rows_out(ctile, c_rsrc(pm0, pn0), (uint32_t)p.ldc, r_base + ks * kStoreRows, lane);
+        }
+        tile_origin(i, pm0, pn0);
+      }
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int st = 0; st < kStoreSteps; ++st) c_rows_out(ctile, c_rsrc(pm0, pn0), (uint32_t)p.ldc, r_base + st * kStoreRows, lane);
+      return;
+    }
+
+    const int wm = wave / WN, wn = wave % WN;
+    const int r16 = lane & 15, g = lane >> 4;
+    auto a_rsrc = [&](int m0) { return make_rsrc(p.a + (int64_t)m0 * p.lda, (uint32_t)BM * (uint32_t)p.lda * 2u); };
+    auto b_rsrc = [&](int n0) {
+      return make_rsrc(p.b + n0, (uint32_t)(((int64_t)(p.K - 1) * p.ldb + (p.N - n0)) * 2));
+    };
+
+    // DMA and read addresses as run() (16x16 layout, K whole slabs).
+    uint32_t aoffs[A_PER_WAVE], boffs[B_PER_WAVE];
+#pragma unroll
+    for (int j = 0; j < A_PER_WAVE; ++j) {
+      const int byte = (wave * A_PER_WAVE + j) * 1024 + lane * 16;
+      const int r = byte / AP, s = (byte % AP) / 16;
+      const int c = s ^ ((r / RA) & (SA - 1));
+      aoffs[j] = ((uint32_t)r * (uint32_t)p.lda + c * 8) * 2u;
+    }
+#pragma unroll
+    for (int j = 0; j < B_PER_WAVE; ++j) {
+      const int byte = (wave * B_PER_WAVE + j) * 1024 + lane * 16;
+      const int k = byte / BP, s = (byte % BP) / 16;
+      const int c = s ^ (2 * ((k & 3) | (((k >> 3) & 1) << 2)));
+      boffs[j] = ((uint32_t)k * (uint32_t)p.ldb + c * 8) * 2u;
+    }
+    uint32_t aaddr[KCH], baddr[TN];
+    {
+      const int xs = (r16 / RA) & (SA - 1);
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) aaddr[c] = (uint32_t)((r16 * AP + 16 * (g ^ xs)) ^ (64 * c));
+      const int kr = 8 * g + (r16 >> 2);
+      const int h = (r16 >> 2) | ((g & 1) << 2);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int jt = wn * TN + tn;
+        baddr[tn] = (uint32_t)(kr * BP + 32 * (jt ^ h) + 8 * (r16 & 3));
+      }
+    }
+
+    const uint32_t a_slab_bytes = (uint32_t)BK * 2u;
+    const uint32_t b_slab_bytes = (uint32_t)BK * (uint32_t)p.ldb * 2u;
+    const uint32_t smem_lds = lds_address(smem);
+
+    int m0c, n0c, m0n = 0, n0n = 0;
+    tile_origin(0, m0c, n0c);
+    bool has_next = n_my > 1;
+    if (has_next) tile_origin(1, m0n, n0n);
+    int gs0 = 0;  // global index of the current tile's slab 0 (its ring slot is (gs0 + ks) % RING)
+    // DMA instruction J of the current tile's slab ks_t; ks_t >= ksteps is the next tile's slab
+    // ks_t - ksteps, or zeros (an offset past the range) when there is none.
+    auto dma_slab = [&](int ks_t, auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      const uint32_t slotb = smem_lds + (uint32_t)((gs0 + ks_t) % RING) * SLAB_BYTES;
+      const bool nxt = ks_t >= ksteps;
+      const uint32_t ks = (uint32_t)(nxt ? ks_t - ksteps : ks_t);
+      const bool live = !nxt | has_next;
+      if constexpr (j < A_PER_WAVE) {
+        const uint32_t off = live ? aoffs[j] + ks * a_slab_bytes : 0x80000000u;
+        buffer_load16_to_lds(a_rsrc(nxt ? m0n : m0c), off, slotb + (wave * A_PER_WAVE + j) * 1024);
+      } else {
+        constexpr int jb = j - A_PER_WAVE;
+        const uint32_t off = live ? boffs[jb] + ks * b_slab_bytes : 0x80000000u;
+        buffer_load16_to_lds(b_rsrc(nxt ? n0n : n0c), off, slotb + A_BYTES + (wave * B_PER_WAVE + jb) * 1024);
+      }
+    };
+
+    // Prologue: the first tile's slabs 0 .. RING - 1 (ksteps >= kStoreSteps >= RING).
+#pragma unroll
+    for (int s0 = 0; s0 < RING; ++s0) {
+      auto d = [&](auto jc) __attribute__((always_inline)) { dma_slab(s0, jc); };
+      dma_all<0>(d);
+    }
+    wait_vm_lds_barrier<(RING - 1) * DMA_PER_SLAB>();
+    Frag f[2];
+    read_frag<0>(f[0], smem, aaddr, baddr, wm);
+
+    for (int i = 0; i < n_my; ++i) {
+      AccTiles acc;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+#pragma unroll
+        for (int q = 0; q < (int)(sizeof(acc.v[0]) / sizeof(floatx16)); ++q)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc.v[tn][q][r] = 0.f;
+#pragma unroll
+        for (int q = 0; q < (int)(sizeof(acc.t[0]) / sizeof(Acc)); ++q)
+#pragma unroll
+          for (int r = 0; r < ACC; ++r) acc.t[tn][q][r] = 0.f;
+      }
+      for (int ks = 0; ks < ksteps; ++ks) {
+        const char* slab = smem + ((gs0 + ks) % RING) * SLAB_BYTES;
+        auto wait = [&]() __attribute__((always_inline)) {
+          wait_vm_lds_barrier<0>();  // slab ks + 1 landed (only slab DMA is in flight)
+          __builtin_amdgcn_sched_barrier(0);
+          return smem + ((gs0 + ks + 1) % RING) * SLAB_BYTES;
+        };
+        auto dma = [&](auto jc) __attribute__((always_inline)) { dma_slab(ks + RING, jc); };
+        chunk_step<0, 0>(acc, f, slab, aaddr, baddr, wm, wait, dma);
+      }
+      // C to LDS for the store waves (they finished reading the previous tile's before this
+      // tile's barrier of step kStoreSteps); the next tile's first slabs and first chunk are
+      // already in flight / read
+      c_to_lds(acc, ctile, wm, wn, lane);
+      if (i + 1 < n_my) {
+        gs0 += ksteps;
+        m0c = m0n;
+        n0c = n0n;
+        has_next = i + 2 < n_my;
+        if (has_next) tile_origin(i + 2, m0n, n0n);
+      } else {
+        wait_vm_lds_barrier<0>();  // the last tile's C is in LDS for the store waves
+      }
+    }
+  }
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
@@ -558,6 +789,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(GemmParams p) {
 template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_shallow_kernel(GemmParams p) {
   GemmKernel<BM, BN, BK, WM, WN, true, MI, SCHED>::run(p);
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
+__global__ __launch_bounds__((WM * WN + kGemmPersistStoreWaves) * 64) void gemm_f16_persist_kernel(GemmParams p) {
+  GemmKernel<BM, BN, BK, WM, WN, false, MI, SCHED>::run_persistent(p);
 }
 
 // The shallow-ring kernel of a tile, or nullptr when its ring would be as deep as the default one.
@@ -573,7 +809,14 @@ const void* gemm_shallow_fn() {
   {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN, MI, SCHED>,                    \
    gemm_shallow_fn<BM, BN, BK, WM, WN, MI, SCHED>(),                                                      \
    "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "ELi" #MI "ELi" #SCHED \
-   "EEEvNS_10GemmParamsE"}
+   "EEEvNS_10GemmParamsE", nullptr}
+// A tile that also has the persistent short-K kernel.
+#define GEMM_ENTRY_PERSIST(BM, BN, BK, WM, WN, MI, SCHED)                                                 \
+  {BM, BN, BK, WM * WN, (const void*)&gemm_f16_kernel<BM, BN, BK, WM, WN, MI, SCHED>,                    \
+   gemm_shallow_fn<BM, BN, BK, WM, WN, MI, SCHED>(),                                                      \
+   "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "ELi" #MI "ELi" #SCHED \
+   "EEEvNS_10GemmParamsE",                                                                                \
+   (const void*)&gemm_f16_persist_kernel<BM, BN, BK, WM, WN, MI, SCHED>}
 
 // One kernel per tile: the MFMA shape and schedule measured fastest for it on MI355X (16x16x32
 // MFMAs draw less power per flop, which raises the clock of the 8-wave tiles; the pipelined
@@ -581,7 +824,7 @@ const void* gemm_shallow_fn() {
 static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(256, 256, 64, 2, 4, 16, 1),
     GEMM_ENTRY(256, 256, 32, 2, 4, 16, 1),
-    GEMM_ENTRY(256, 128, 64, 2, 4, 16, 1),
+    GEMM_ENTRY_PERSIST(256, 128, 64, 2, 4, 16, 1),
     GEMM_ENTRY(128, 256, 64, 2, 4, 16, 1),
     GEMM_ENTRY(256, 256, 64, 2, 2, 32, 1),
     GEMM_ENTRY(256, 256, 32, 2, 2, 32, 1),

@@ -159,3 +159,39 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(hip_lib, "LIB_PATH", tmp_path / "libfa_gfx950.so")
     with pytest.raises(hip_lib.FaLibraryError, match="missing"):
         hip_lib.load()
+
+
+_ASM_LOAD = """_ZN2fa6kernelEv:
+{pre}
+	;;#ASMSTART
+{guard}	s_mov_b32 m0, s20
+	buffer_load_dwordx4 v163, s[12:15], 0 offen offset:0 lds
+	;;#ASMEND
+	s_endpgm
+"""
+
+
+@pytest.mark.parametrize("pre,guard,hits", [
+    ("\tv_readlane_b32 s15, v166, 7", "", 1),             # VALU writes the descriptor, load 0 wait states later
+    ("\tv_readfirstlane_b32 s13, v2\n\ts_mov_b32 s1, 0\n\ts_mov_b32 s2, 0", "", 1),  # 2 wait states
+    ("\tv_readlane_b32 s15, v166, 7", "\ts_nop 4\n", 0),  # the guard: 5 wait states
+    ("\tv_readfirstlane_b32 s13, v2\n" + "\ts_add_u32 s0, s0, 1\n" * 5, "", 0),  # 5 instructions between
+    ("\ts_mov_b32 s15, s3", "", 0),                        # a scalar write is no hazard
+    ("\tv_readlane_b32 s30, v166, 7", "", 0),              # an SGPR the load does not read
+])
+def test_build_asm_hazard_check_loads(pre, guard, hits):
+    """The build's assembly check (build_lib.asm_hazards) flags a VALU write to an SGPR that an
+    inline-asm vector-memory instruction reads within 5 wait states, and nothing else."""
+    import build_lib
+    asm = _ASM_LOAD.format(pre=pre, guard=guard)
+    assert len(build_lib.asm_hazards(asm)) == hits
+
+
+@pytest.mark.parametrize("inside,hits", [("", 1), ("\ts_nop 1\n", 0)])
+def test_build_asm_hazard_check_wide_stores(inside, hits):
+    """An inline-asm store of 16 bytes must end in an s_nop: a VALU write to its data registers right
+    after it corrupts the stored data (seen in the persistent GEMM's first version)."""
+    import build_lib
+    asm = ("_ZN2fa6kernelEv:\n\t;;#ASMSTART\n\tbuffer_store_dwordx4 v[24:27], v29, s[8:11], 0 offen\n"
+           + inside + "\t;;#ASMEND\n\tv_add_u32_e32 v24, v23, v30\n")
+    assert len(build_lib.asm_hazards(asm)) == hits

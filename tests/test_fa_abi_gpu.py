@@ -389,3 +389,46 @@ def _compare_resources(live: dict, raw: dict, waves: int) -> None:
     assert live["occupancy"] == raw["Occupancy [waves/SIMD]"]
     assert live["lds_bytes"] == raw["LDS Size [bytes/block]"]
     assert live["threads"] == waves * 64 <= live["max_threads"]
+
+
+# Shapes that run the persistent short-K GEMM kernel of the 256x128x64 8-wave tile (whole tiles,
+# 4..16 K slabs, a tile count divisible by 8): many tiles per workgroup, an uneven share (272 tiles
+# over 256 workgroups), one tile each, an odd slab count, the longest K it takes, GROUP_M 1 / 4 / 8.
+PERSIST_GEMM_CASES = [(8192, 8192, 256, 8), (4352, 2048, 256, 4), (2048, 1024, 256, 8), (4096, 1024, 320, 1),
+                      (1024, 2048, 1024, 8), (4096, 4096, 512, 4)]
+
+
+@pytest.mark.parametrize("M,N,K,gm", PERSIST_GEMM_CASES)
+def test_gemm_persistent_matches_per_tile_kernel(gpu, M, N, K, gm):
+    """The persistent kernel (16-byte aligned C) against the same tile's one-workgroup-per-tile
+    kernel (C 8 bytes off 16-byte alignment, which the persistent kernel does not take): identical
+    accumulation order and rounding, so the results must be bit-identical."""
+    print(f"[gemm_abi] persistent M={M} N={N} K={K} group_m={gm}", flush=True)
+    g = torch.Generator(device="cuda:0").manual_seed(M + N + K)
+    a = (torch.rand((M, K), generator=g, device="cuda:0") * 2 - 1).half()
+    b = (torch.rand((K, N), generator=g, device="cuda:0") * 2 - 1).half()
+    tile = hip_lib.GemmTile(256, 128, 64, 8, gm)
+    c = torch.full((M, N), float("nan"), dtype=F16, device="cuda:0")
+    assert c.data_ptr() % 16 == 0
+    hip_lib.gemm_f16(a, b, c, tile)
+    raw = torch.full((M * N + 4,), float("nan"), dtype=F16, device="cuda:0")
+    c8 = raw[4:].view(M, N)
+    assert c8.data_ptr() % 16 == 8
+    hip_lib.gemm_f16(a, b, c8, tile)
+    torch.cuda.synchronize()
+    assert not torch.isnan(c).any()
+    assert torch.equal(c, c8)
+
+
+def test_gemm_persistent_against_oracle(gpu):
+    """The persistent kernel on a small shape against the exact oracle product."""
+    M, N, K = 2048, 1024, 320
+    print(f"[gemm_abi] persistent oracle M={M} N={N} K={K}", flush=True)
+    a = oracle.round_to(oracle.portable_uniform(21, (M, K), -1, 1), 0)
+    b = oracle.round_to(oracle.portable_uniform(22, (K, N), -1, 1), 0)
+    cd = torch.empty((M, N), dtype=F16, device="cuda:0")
+    hip_lib.gemm_f16(to_device(a, F16, "cuda:0"), to_device(b, F16, "cuda:0"), cd, hip_lib.GemmTile(256, 128, 64, 8, 8))
+    torch.cuda.synchronize()
+    ref = oracle.gemm(a, b)
+    c = cd.float().cpu().numpy()
+    assert float(np.linalg.norm(c - ref) / np.linalg.norm(ref)) <= 1e-3
