@@ -69,19 +69,22 @@ def _time(fn, warmup: int, iters: int, batch_ms: float = 1.0) -> float:
 
 REFINE_TOP = 3
 REFINE_ROUNDS = 5
+REFINE_BATCH_MS = 8.0
 
 
 def _refine(fns: dict, results: dict, top: int = REFINE_TOP, rounds: int = REFINE_ROUNDS, iters: int = 3) -> dict:
     """Re-time the `top` fastest candidates of a first pass in `rounds` interleaved rounds and
     return their medians: tiles within a few percent of each other are then ranked under the same
-    clock and thermal conditions rather than by one pass each, minutes apart."""
+    clock and thermal conditions rather than by one pass each, minutes apart. Each sample is a
+    batch of ~REFINE_BATCH_MS of back-to-back launches (a 2 ms kernel timed one launch per sample
+    ranked two tiles 2% apart the wrong way round)."""
     best = sorted(results, key=results.get)[:top]
     if len(best) < 2:
         return {}
     samples: dict = {k: [] for k in best}
     for _ in range(rounds):
         for k in best:
-            samples[k].append(_time(fns[k], 1, iters))
+            samples[k].append(_time(fns[k], 1, iters, batch_ms=REFINE_BATCH_MS))
     return {k: round(statistics.median(v), 4) for k, v in samples.items()}
 
 
