@@ -829,7 +829,7 @@ const void* gemm_shallow_fn() {
 static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(256, 256, 64, 2, 4, 16, 1),
     GEMM_ENTRY(256, 256, 32, 2, 4, 16, 1),
-    GEMM_ENTRY_PERSIST(256, 128, 64, 2, 4, 16, 1),
+    GEMM_ENTRY_PERSIST(256, 128, 64, 4, 2, 16, 1),
     GEMM_ENTRY(128, 256, 64, 2, 4, 16, 1),
     GEMM_ENTRY(256, 256, 64, 2, 2, 32, 1),
     GEMM_ENTRY(256, 256, 32, 2, 2, 32, 1),
