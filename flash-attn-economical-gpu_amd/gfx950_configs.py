@@ -251,6 +251,41 @@ def _nearest_fa_entry(table: dict, key: str) -> dict | None:
     return best
 
 
+def _nearest_gemm_entry(table: dict, key: str) -> dict | None:
+    """The entry for `key` ("M..|N..|K.."), else the swept GEMM bucket nearest to it: smallest sum
+    of |log2| distances in M, N and K (ties: more work, then key order). A shape between the swept
+    sizes (1024x4096x1024, say) then runs a tile timed on a shape of its scale, not the first built
+    tile -- a 256x256 tile there leaves three quarters of the CUs idle."""
+    entry = table.get(key)
+    if entry is not None:
+        return entry
+    want = [int(part.lstrip("MNK")) for part in key.split("|")]
+    best, best_rank = None, None
+    for other, ent in sorted(table.items()):
+        have = [int(part.lstrip("MNK")) for part in other.split("|")]
+        dist = sum(abs(math.log2(a) - math.log2(b)) for a, b in zip(want, have))
+        rank = (dist, -have[0] * have[1] * have[2])
+        if best_rank is None or rank < best_rank:
+            best, best_rank = ent, rank
+    return best
+
+
+def _gemm_ranked_tiles(entry: dict) -> list[tuple[tuple[int, ...], int]]:
+    """(tile, group_m) of a GEMM table entry, fastest first: the entry's winner, then every other
+    timed (tile, GROUP_M) in order of its time."""
+    ranked = [(tuple(entry["tile"]), int(entry.get("group_m", GEMM_DEFAULT_GROUP_M)))]
+    timed = {**entry.get("timed", {}), **entry.get("refined", {})}
+    for name in sorted(timed, key=timed.get):
+        tile_part, _, gm_part = name.partition("g")
+        try:
+            item = (tuple(int(x) for x in tile_part.split("x")), int(gm_part))
+        except ValueError:
+            continue
+        if item not in ranked:
+            ranked.append(item)
+    return ranked
+
+
 def choose_fa_tile(variant: int, dtype, D: int, causal: bool, B: int, H: int, M: int, N: int,
                    candidates: list[FaTileChoice]) -> FaTileChoice:
     """Timed-table winner among candidates (the shape's bucket, else its nearest swept bucket of the
@@ -335,11 +370,13 @@ def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None =
         if not hinted and len(hint) > 3:  # no built tile with that wave count: keep the sizes
             hinted = [t for t in cands if t[:3] == hint[:3]]
         cands = hinted or cands
-    entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
+    # the bucket's (or nearest swept bucket's) winner when it divides, else its fastest timed tile
+    # that does; the preference order only without a table
+    entry = _nearest_gemm_entry(load_tune_table()["gemm"], gemm_table_key(M, N, K))
     if entry is not None:
-        for t in cands:
-            if list(t) == list(entry["tile"]):
-                return (*t, int(entry.get("group_m", GEMM_DEFAULT_GROUP_M)))
+        for tile, group_m in _gemm_ranked_tiles(entry):
+            if tile in cands:
+                return (*tile, group_m)
     t = cands[0]
     return (*t, _gemm_group_m(M, N, K, t))
 
@@ -356,11 +393,11 @@ def choose_gemm_tile_any(M: int, N: int, K: int) -> tuple[int, int, int, int, in
     except ValueError:
         pass
     cands = gemm_candidates()
-    entry = load_tune_table()["gemm"].get(gemm_table_key(M, N, K))
+    entry = _nearest_gemm_entry(load_tune_table()["gemm"], gemm_table_key(M, N, K))
     if entry is not None:
-        for t in cands:
-            if list(t) == list(entry["tile"]):
-                return (*t, int(entry.get("group_m", GEMM_DEFAULT_GROUP_M)))
+        for tile, group_m in _gemm_ranked_tiles(entry):
+            if tile in cands:
+                return (*tile, group_m)
     fit = [t for t in cands if t[0] <= -(-M // 64) * 64 and t[1] <= -(-N // 64) * 64]
     t = (fit or [min(cands, key=lambda t: t[0] * t[1])])[0]
     return (*t, GEMM_DEFAULT_GROUP_M)

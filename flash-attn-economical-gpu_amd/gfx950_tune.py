@@ -46,25 +46,44 @@ GEMM_SWEEP = ([(n, n, n) for n in (1024, 2048, 4096, 8192, 16384)]
 GROUP_MS = (4, 8, 16)
 
 
+GRAPH_BELOW_MS = 0.25
+
+
 def _time(fn, warmup: int, iters: int, batch_ms: float = 1.0) -> float:
     """Median per-launch time (ms) of back-to-back launches: each of `iters` samples times a batch
     of launches lasting about `batch_ms`, so short kernels are ranked by their steady rate rather
-    than by one launch from an idle queue."""
+    than by one launch from an idle queue. A launch shorter than GRAPH_BELOW_MS is timed as a
+    replay of the batch captured in a HIP graph: eager launches of a few microseconds are paced by
+    the host's per-call cost (~6 us here), not by the kernel, which would tie every tile."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
 
-    def sample(n: int) -> float:
+    def sample(run, n: int) -> float:
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(n):
-            fn()
+        run()
         e.record()
         torch.cuda.synchronize()
         return s.elapsed_time(e) / n
 
-    batch = max(1, min(64, round(batch_ms / max(sample(1), 1e-3))))
-    return statistics.median(sample(batch) for _ in range(iters))
+    def eager(n: int):
+        def run():
+            for _ in range(n):
+                fn()
+        return run
+
+    one = sample(eager(1), 1)
+    batch = max(1, min(64, round(batch_ms / max(one, 1e-3))))
+    if one < GRAPH_BELOW_MS:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(batch):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        return statistics.median(sample(graph.replay, batch) for _ in range(iters))
+    return statistics.median(sample(eager(batch), batch) for _ in range(iters))
 
 
 REFINE_TOP = 3

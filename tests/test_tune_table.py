@@ -138,6 +138,30 @@ def test_shape_without_bucket_takes_nearest_swept_bucket(tmp_path, monkeypatch, 
                                cfgs.fa_candidates(opt, torch.bfloat16, 128)) == cfgs.fa_candidates(opt, torch.bfloat16, 128)[0]
 
 
+def test_gemm_shape_without_bucket_takes_nearest_swept_bucket(tmp_path, monkeypatch, fresh_table_cache):
+    """A GEMM shape between the swept buckets runs the winner of the nearest one (sum of |log2|
+    distances in M, N, K); when that winner does not divide the shape, the fastest tile it timed
+    that does."""
+    small, big = cfgs.gemm_table_key(1024, 1024, 1024), cfgs.gemm_table_key(8192, 8192, 8192)
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"fa": {}, "gemm": {
+        small: {"tile": [128, 64, 32, 4], "group_m": 8,
+                "timed": {"128x64x32x4g8": 0.0106, "128x128x32x4g4": 0.0107, "256x256x64x8g8": 0.0231}},
+        big: {"tile": [256, 256, 64, 8], "group_m": 8, "timed": {"256x256x64x8g8": 0.8, "128x128x32x4g4": 1.1}},
+    }}))
+    monkeypatch.setattr(cfgs, "TUNE_TABLE_PATH", path)
+    # 1024x4096x1024: two octaves from `small`, five from `big`
+    assert cfgs.choose_gemm_tile(1024, 4096, 1024) == (128, 64, 32, 4, 8)
+    assert cfgs.choose_gemm_tile(16384, 8192, 4096) == (256, 256, 64, 8, 8)
+    # N = 1152 (bucket 2048) is nearest `small`, whose winner 128x64 divides it
+    assert cfgs.choose_gemm_tile(1024, 1152, 1024) == (128, 64, 32, 4, 8)
+    # M = 1152 (bucket 2048) with N = K = 8192 is nearest `big`, whose winner 256x256 does not
+    # divide M: the next tile `big` timed, 128x128 with its GROUP_M, does
+    assert cfgs.choose_gemm_tile(1152, 8192, 8192) == (128, 128, 32, 4, 4)
+    # ragged shapes take the same ranking without the divisibility filter
+    assert cfgs.choose_gemm_tile_any(1000, 4000, 1000)[:4] == (128, 64, 32, 4)
+
+
 def test_table_entry_for_unbuilt_tile_is_ignored(tmp_path, monkeypatch, fresh_table_cache):
     key = cfgs.fa_table_key(hip_lib.FA_VARIANT_OPT, torch.float16, 128, False, 4, 32, 8192, 8192)
     path = tmp_path / "t.json"
