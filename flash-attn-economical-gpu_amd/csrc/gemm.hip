@@ -66,10 +66,13 @@ struct GemmAcc<16> {
 
 // MI: MFMA shape (32: v_mfma_f32_32x32x16_f16, 16: v_mfma_f32_16x16x32_f16). SCHED: 0 = one fragment
 // buffer per chunk, scheduled by the compiler; 1 = fragments double-buffered across chunks and
-// slabs, LDS-DMA spread over the last chunk's MFMAs.
-template <int BM, int BN, int BK, int WM, int WN, bool SHALLOW, int MI, int SCHED>
+// slabs, LDS-DMA spread over the last chunk's MFMAs. KSG: K groups -- the workgroup holds KSG groups
+// of WM x WN waves, group g multiplying its own contiguous run of the K slabs through its own LDS
+// ring; the partial sums of groups 1.. are added into group 0's through LDS before the epilogue
+// (a short serial K loop and more waves per CU for shapes with few tiles).
+template <int BM, int BN, int BK, int WM, int WN, bool SHALLOW, int MI, int SCHED, int KSG = 1>
 struct GemmKernel {
-  static constexpr int WAVES = WM * WN;
+  static constexpr int WAVES = WM * WN;  // waves of one K group
   static constexpr int KD = MI == 32 ? 16 : 32;  // k depth of one MFMA
   static constexpr int TM = BM / WM / MI;        // MI-row tiles per wave along M
   static constexpr int TN = BN / WN / MI;        // MI-col tiles per wave along N
@@ -120,10 +123,11 @@ struct GemmKernel {
   static constexpr int A_BYTES = BM * AP;
   static constexpr int B_BYTES = BK * BP;
   static constexpr int SLAB_BYTES = A_BYTES + B_BYTES;
-  // Slabs resident in LDS: as many as fit in 128 KiB, 2..4. The SHALLOW variant keeps the fewest
+  // Slabs resident in LDS: as many as fit in 128 KiB, 2..4 (with K groups, as many as fit in each
+  // group's share of 160 KiB). The SHALLOW variant keeps the fewest
   // that still hold the staged C tile (at least 2): less LDS per workgroup, so more workgroups
   // share a CU, which pays when K is only a few slabs deep (their latency is then the cost).
-  static constexpr int RING_FIT = 131072 / SLAB_BYTES;
+  static constexpr int RING_FIT = KSG == 1 ? 131072 / SLAB_BYTES : 163840 / KSG / SLAB_BYTES;
   static constexpr int RING_DEEP = RING_FIT > 4 ? 4 : (RING_FIT < 2 ? 2 : RING_FIT);
   static constexpr int RING_C = (BM * BN * 2 + SLAB_BYTES - 1) / SLAB_BYTES;
   static constexpr int RING = SHALLOW ? (RING_C > 2 ? RING_C : 2) : RING_DEEP;
@@ -142,7 +146,36 @@ struct GemmKernel {
   static_assert(RING * SLAB_BYTES <= 160 * 1024, "LDS");
   static constexpr int CP = BN * 2;                      // C tile row pitch in LDS (bytes)
   static constexpr int CHS = CP / 16 < 16 ? CP / 16 : 16;  // swizzled 16-byte chunks per C row
-  static_assert(BM * CP <= RING * SLAB_BYTES, "the C tile is staged in the slab ring");
+  static_assert(KSG > 1 || BM * CP <= RING * SLAB_BYTES, "the C tile is staged in the slab ring");
+  // K groups: after the K loop the LDS holds the staged C tile and, behind it, the partial sums of
+  // groups 1 .. KSG-1 (each wave's accumulators as NQ lane-major 16-byte pieces).
+  static constexpr int NV = AG == 4 ? TM / 4 : (MI == 32 ? TM : 1);  // floatx16 tuples per B block
+  static constexpr int NQ = TN * ((MI == 32 || AG == 4) ? NV * 4 : TM);  // accumulator float4s per lane
+  static constexpr int CT_BYTES = BM * CP;
+  static constexpr int PART_BYTES = (KSG - 1) * WAVES * NQ * 1024;
+  static constexpr int RING_BYTES = KSG * RING * SLAB_BYTES;
+  static constexpr int SMEM_BYTES = RING_BYTES > CT_BYTES + PART_BYTES ? RING_BYTES : CT_BYTES + PART_BYTES;
+  static_assert(KSG == 1 || (kPipe && !SHALLOW), "K groups: the pipelined per-tile kernel only");
+  static_assert(KSG >= 1 && SMEM_BYTES <= 160 * 1024, "LDS");
+  static_assert(NQ == TM * TN * MI * MI / 256, "accumulator pieces cover the wave's tile");
+
+  // The accumulators as NQ pieces of 4 consecutive floats: f(q, tuple, offset) for piece q, which is
+  // elements offset .. offset + 3 of `tuple` (a floatx16 or floatx4 register tuple, by reference).
+  template <class F>
+  __device__ __attribute__((always_inline)) static inline void acc_quads(AccTiles& acc, F&& f) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      if constexpr (MI == 32 || AG == 4) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) f((tn * NV + i) * 4 + r, acc.v[tn][i], 4 * r);
+      } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) f(tn * TM + i, acc.t[tn][i], 0);
+      }
+    }
+  }
 
   // Fragments of one KD-deep chunk: TM A^T column blocks (ds_read_b128) and TN B^T row blocks (two
   // transposing reads each).
@@ -291,9 +324,12 @@ struct GemmKernel {
   }
 
   __device__ static void run(const GemmParams& p) {
-    __shared__ __attribute__((aligned(16))) char smem[RING * SLAB_BYTES];
+    __shared__ __attribute__((aligned(16))) char smem[SMEM_BYTES];
     const int tid = (int)__builtin_amdgcn_workitem_id_x();
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    // K group kg of the workgroup, wave wl of it (without K groups: 0 and the wave)
+    const int kg = KSG == 1 ? 0 : __builtin_amdgcn_readfirstlane((tid >> 6) / WAVES);
+    const int wave = KSG == 1 ? tid >> 6 : (tid >> 6) % WAVES;
     const int col = lane & 31, hh = lane >> 5;
     const int wm = wave / WN, wn = wave % WN;
 
@@ -438,18 +474,26 @@ struct GemmKernel {
       // DMA instruction J of slab ks, branch-free: past the last slab it reads an offset beyond the
       // range, so the slot holds zeros, and exactly RING - 2 slabs are always in flight behind the
       // one a barrier waits for.
+      // K group kg multiplies slabs kbase .. kbase + per - 1 (its step ks is slab kbase + ks) in its
+      // own ring; all groups take the same steps and barriers, a group's steps past its run or past
+      // K multiplying zeros.
+      const int per = KSG == 1 ? ksteps : (ksteps + KSG - 1) / KSG;
+      const int kbase = kg * per;
+      const uint32_t ring_lds = smem_lds + (uint32_t)(kg * RING * SLAB_BYTES);
+      const char* const ring = smem + kg * RING * SLAB_BYTES;
       auto dma_slab = [&](int ks, auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
-        const uint32_t slot = smem_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
-        const bool live = ks < ksteps;
+        const uint32_t slot = ring_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
+        const int gk = kbase + ks;
+        const bool live = (ks < per) & (gk < ksteps);
         if constexpr (j < A_PER_WAVE) {
           // bitwise, not short-circuit: the scalar and per-lane parts stay one select
-          const bool zero = !live | (k_ragged & (ks == ksteps - 1) & (ks * BK + ak0[j] >= p.K));
-          const uint32_t off = zero ? 0x80000000u : aoffs[j] + (uint32_t)ks * a_slab_bytes;
+          const bool zero = !live | (k_ragged & (gk == ksteps - 1) & (gk * BK + ak0[j] >= p.K));
+          const uint32_t off = zero ? 0x80000000u : aoffs[j] + (uint32_t)gk * a_slab_bytes;
           buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
         } else {
           constexpr int jb = j - A_PER_WAVE;
-          const uint32_t off = live ? boffs[jb] + (uint32_t)ks * b_slab_bytes : 0x80000000u;
+          const uint32_t off = live ? boffs[jb] + (uint32_t)gk * b_slab_bytes : 0x80000000u;
           buffer_load16_to_lds(brs, off, slot + A_BYTES + (wave_u * B_PER_WAVE + jb) * 1024);
         }
       };
@@ -462,28 +506,28 @@ struct GemmKernel {
       }
       wait_vm_lds_barrier<(RING - 1) * DMA_PER_SLAB>();
       Frag f[2];
-      read_frag<0>(f[0], smem, aaddr, baddr, wm);
+      read_frag<0>(f[0], ring, aaddr, baddr, wm);
       // Every slab takes the same step (barrier, refill, next slab's first reads): the last one
       // reads a slab that is never multiplied. Slab ks's chunk 0 uses buffer (ks * KCH) & 1, so with an
       // odd chunk count slabs go in pairs and an odd slab count gets one more slab, which the
       // branch-free DMA fills with zeros (its products add exactly 0). No tail code: the epilogue
       // starts with only the accumulators live.
       auto slab_step = [&](int ks, auto par_c) __attribute__((always_inline)) {
-        const char* slab = smem + (ks % RING) * SLAB_BYTES;
+        const char* slab = ring + (ks % RING) * SLAB_BYTES;
         // Slab ks+1 must have landed; the RING - 2 slabs after it stay in flight.
         auto wait = [&]() __attribute__((always_inline)) {
           wait_vm_lds_barrier<(RING - 2) * DMA_PER_SLAB>();
           __builtin_amdgcn_sched_barrier(0);
-          return smem + ((ks + 1) % RING) * SLAB_BYTES;
+          return ring + ((ks + 1) % RING) * SLAB_BYTES;
         };
         // Slab ks + RING goes into slab ks's slot: every wave passed the barrier.
         auto dma = [&](auto jc) __attribute__((always_inline)) { dma_slab(ks + RING, jc); };
         chunk_step<(decltype(par_c)::value * KCH) & 1, 0>(acc, f, slab, aaddr, baddr, wm, wait, dma);
       };
       if constexpr (KCH % 2 == 0) {
-        for (int ks = 0; ks < ksteps; ++ks) slab_step(ks, std::integral_constant<int, 0>{});
+        for (int ks = 0; ks < per; ++ks) slab_step(ks, std::integral_constant<int, 0>{});
       } else {
-        for (int ks = 0; ks < ksteps; ks += 2) {
+        for (int ks = 0; ks < per; ks += 2) {
           slab_step(ks, std::integral_constant<int, 0>{});
           slab_step(ks + 1, std::integral_constant<int, 1>{});
         }
@@ -504,36 +548,67 @@ struct GemmKernel {
       }
     }
 
+    if constexpr (KSG > 1) {
+      // Partial sums of groups 1 .. KSG-1 into group 0's accumulators, through LDS behind the C
+      // staging area (the ring is free: every wave passed the last step's barrier with its DMA and
+      // LDS reads done). Each wave's piece q sits at q * 1 KiB + lane * 16 of its own block, so
+      // every write and read instruction covers 1 KiB contiguously.
+      char* const part = smem + CT_BYTES;
+      if (kg > 0) {
+        char* const mine = part + ((kg - 1) * WAVES + wave) * NQ * 1024 + lane * 16;
+        acc_quads(acc, [&](int q, auto& t, int o) __attribute__((always_inline)) {
+          *reinterpret_cast<floatx4*>(mine + q * 1024) = (floatx4){t[o], t[o + 1], t[o + 2], t[o + 3]};
+        });
+      }
+      __syncthreads();
+      if (kg == 0) {
+#pragma unroll
+        for (int g = 1; g < KSG; ++g) {
+          const char* const src = part + ((g - 1) * WAVES + wave) * NQ * 1024 + lane * 16;
+          acc_quads(acc, [&](int q, auto& t, int o) __attribute__((always_inline)) {
+            const floatx4 x = *reinterpret_cast<const floatx4*>(src + q * 1024);
+            t[o] += x[0];
+            t[o + 1] += x[1];
+            t[o + 2] += x[2];
+            t[o + 3] += x[3];
+          });
+        }
+      }
+    }
+
     // C goes out through LDS (the ring is free after the last step's barrier): each lane holds 4
     // consecutive columns of one row per 32x32 tile (C^T layout), which as direct 8-byte stores
     // left C lines written in pieces; staged in LDS, each lane stores 16 contiguous bytes and 8
     // lanes a full 128-byte line. LDS rows are XOR-swizzled in 16-byte chunks
     // (chunk ^ (row & (CHS - 1))), so the 32 rows one write instruction touches spread over the banks.
+    // With K groups, group 0 (holding the sums) stages the tile and every wave stores it.
     char* ctile = smem;
+    if (KSG == 1 || kg == 0) {
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      // 32x32: lane holds row col, columns 8 gq + 4 hh + 0..3; 16x16: row lane & 15, columns
-      // 4 (lane >> 4) + 0..3.
-      const int r = (wm * TM + tm) * MI + (MI == 32 ? col : (lane & 15));
+      for (int tm = 0; tm < TM; ++tm) {
+        // 32x32: lane holds row col, columns 8 gq + 4 hh + 0..3; 16x16: row lane & 15, columns
+        // 4 (lane >> 4) + 0..3.
+        const int r = (wm * TM + tm) * MI + (MI == 32 ? col : (lane & 15));
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
+        for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-        for (int gq = 0; gq < ACC / 4; ++gq) {
-          const int cb = MI == 32 ? ((wn * TN + tn) * 32 + 8 * gq + 4 * hh) * 2   // byte column in the tile row
-                                  : ((wn * TN + tn) * 16 + 4 * (lane >> 4)) * 2;
-          const int phys = r * CP + ((((cb >> 4) ^ (r & (CHS - 1)))) << 4) + (cb & 15);
-          *reinterpret_cast<u32x2*>(ctile + phys) =
-              (u32x2){DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq), acc_at(acc, tn, tm, 4 * gq + 1)),
-                      DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq + 2), acc_at(acc, tn, tm, 4 * gq + 3))};
-        }
+          for (int gq = 0; gq < ACC / 4; ++gq) {
+            const int cb = MI == 32 ? ((wn * TN + tn) * 32 + 8 * gq + 4 * hh) * 2   // byte column in the tile row
+                                    : ((wn * TN + tn) * 16 + 4 * (lane >> 4)) * 2;
+            const int phys = r * CP + ((((cb >> 4) ^ (r & (CHS - 1)))) << 4) + (cb & 15);
+            *reinterpret_cast<u32x2*>(ctile + phys) =
+                (u32x2){DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq), acc_at(acc, tn, tm, 4 * gq + 1)),
+                        DT<f16_t>::pack2(acc_at(acc, tn, tm, 4 * gq + 2), acc_at(acc, tn, tm, 4 * gq + 3))};
+          }
+      }
     }
     __syncthreads();
     // 16-byte global stores need C and its row stride 16-byte aligned (the ABI guarantees 8).
     const bool c16 = ((reinterpret_cast<uintptr_t>(p.c) & 15) == 0) && ((p.ldc & 7) == 0);
     constexpr int CHUNKS = BM * CP / 16;  // 16-byte chunks of the C tile
-    static_assert(CHUNKS % (WAVES * 64) == 0, "C tile chunks split evenly over the threads");
+    static_assert(CHUNKS % (WAVES * KSG * 64) == 0, "C tile chunks split evenly over the threads");
 #pragma unroll 4
-    for (int i = tid; i < CHUNKS; i += WAVES * 64) {
+    for (int i = tid; i < CHUNKS; i += WAVES * KSG * 64) {
       const int r = i / (CP / 16), c = i % (CP / 16);
       const int m = m0 + r, n = n0 + c * 8;
       if (m >= p.M || n >= p.N) continue;
@@ -804,6 +879,11 @@ __global__ __launch_bounds__((WM * WN + kGemmPersistStoreWaves) * 64) void gemm_
   GemmKernel<BM, BN, BK, WM, WN, false, MI, SCHED>::run_persistent(p);
 }
 
+template <int BM, int BN, int BK, int WM, int WN, int MI, int KSG>
+__global__ __launch_bounds__(WM * WN * KSG * 64) void gemm_f16_ksplit_kernel(GemmParams p) {
+  GemmKernel<BM, BN, BK, WM, WN, false, MI, 1, KSG>::run(p);
+}
+
 // The shallow-ring kernel of a tile, or nullptr when its ring would be as deep as the default one.
 template <int BM, int BN, int BK, int WM, int WN, int MI, int SCHED>
 const void* gemm_shallow_fn() {
@@ -825,6 +905,11 @@ const void* gemm_shallow_fn() {
    "_ZN2fa15gemm_f16_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "ELi" #MI "ELi" #SCHED \
    "EEEvNS_10GemmParamsE",                                                                                \
    (const void*)&gemm_f16_persist_kernel<BM, BN, BK, WM, WN, MI, SCHED>}
+// A tile of KSG K groups of WM x WN waves (pipelined schedule; no shallow or persistent kernel).
+#define GEMM_ENTRY_KSPLIT(BM, BN, BK, WM, WN, MI, KSG)                                                    \
+  {BM, BN, BK, WM * WN * KSG, (const void*)&gemm_f16_ksplit_kernel<BM, BN, BK, WM, WN, MI, KSG>, nullptr, \
+   "_ZN2fa22gemm_f16_ksplit_kernelILi" #BM "ELi" #BN "ELi" #BK "ELi" #WM "ELi" #WN "ELi" #MI "ELi" #KSG \
+   "EEEvNS_10GemmParamsE", nullptr}
 
 // One kernel per tile: the MFMA shape and schedule measured fastest for it on MI355X (16x16x32
 // MFMAs draw less power per flop, which raises the clock of the 8-wave tiles; the pipelined
@@ -840,6 +925,9 @@ static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY(128, 128, 32, 2, 2, 32, 1),
     GEMM_ENTRY(128, 64, 32, 2, 2, 32, 0),
     GEMM_ENTRY(64, 256, 32, 2, 2, 16, 1),
+    GEMM_ENTRY_KSPLIT(128, 128, 32, 2, 2, 32, 2),
+    GEMM_ENTRY_KSPLIT(128, 64, 32, 2, 2, 32, 2),
+    GEMM_ENTRY_KSPLIT(128, 64, 32, 2, 2, 32, 4),
 };
 
 const GemmKernelEntry* gemm_registry(int* count) {

@@ -96,6 +96,10 @@ GEMM_TILE_SPACE = [
     (128, 128, 32, 4),
     (128, 64, 32, 4),
     (64, 256, 32, 4),
+    # K groups: 2 or 4 groups of 4 waves split one tile's K loop (shapes with few tiles)
+    (128, 128, 32, 8),
+    (128, 64, 32, 8),
+    (128, 64, 32, 16),
 ]
 GEMM_DEFAULT_GROUP_M = 8
 

@@ -283,7 +283,8 @@ def test_gemm_parity(gpu):
     for (M, N, K, tile) in [(256, 256, 256, (256, 256, 64, 4, 8)), (512, 384, 320, (128, 128, 64, 4, 8)),
                             (1024, 1024, 256, (128, 256, 64, 8, 8)), (512, 512, 512, (256, 256, 32, 8, 8)),
                             (768, 512, 640, (256, 256, 64, 8, 3)), (256, 192, 96, (128, 64, 32, 4, 2)),
-                            (128, 512, 64, (64, 256, 32, 4, 1))]:
+                            (128, 512, 64, (64, 256, 32, 4, 1)), (256, 256, 1024, (128, 128, 32, 8, 4)),
+                            (384, 192, 992, (128, 64, 32, 8, 2)), (256, 128, 1056, (128, 64, 32, 16, 8))]:
         print(f"[gemm_abi] M={M} N={N} K={K} tile={tile}", flush=True)
         if M % tile[0] or N % tile[1] or K % tile[2]:
             continue
