@@ -928,6 +928,7 @@ static const GemmKernelEntry kGemmEntries[] = {
     GEMM_ENTRY_KSPLIT(128, 128, 32, 2, 2, 32, 2),
     GEMM_ENTRY_KSPLIT(128, 64, 32, 2, 2, 32, 2),
     GEMM_ENTRY_KSPLIT(128, 64, 32, 2, 2, 32, 4),
+    GEMM_ENTRY_KSPLIT(64, 64, 32, 2, 2, 32, 2),
 };
 
 const GemmKernelEntry* gemm_registry(int* count) {

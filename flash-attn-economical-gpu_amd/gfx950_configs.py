@@ -100,6 +100,7 @@ GEMM_TILE_SPACE = [
     (128, 128, 32, 8),
     (128, 64, 32, 8),
     (128, 64, 32, 16),
+    (64, 64, 32, 8),
 ]
 GEMM_DEFAULT_GROUP_M = 8
 
@@ -359,7 +360,10 @@ def choose_gemm_tile(M: int, N: int, K: int, hint: tuple[int, int, int] | None =
     (M % 128 == 0 and N % 64 == 0) or (M % 64 == 0 and N % 256 == 0)."""
     if K % 32 != 0:
         raise ValueError("fast 2D contiguous matmul requires K % 32 == 0")
-    cands = [t for t in gemm_candidates() if M % t[0] == 0 and N % t[1] == 0 and K % t[2] == 0]
+    # the reference's rule, stated here rather than left to the built tile set (a 64x64 tile
+    # divides shapes the reference rejects)
+    reference_ok = (M % 128 == 0 and N % 64 == 0) or (M % 64 == 0 and N % 256 == 0)
+    cands = [t for t in gemm_candidates() if M % t[0] == 0 and N % t[1] == 0 and K % t[2] == 0] if reference_ok else []
     if not cands:
         raise ValueError(
             "fast 2D contiguous matmul requires a supported divisible tile: "

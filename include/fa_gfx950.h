@@ -108,9 +108,9 @@ typedef struct {
 } fa_fwd_args;
 
 /* GEMM tile configuration: block_m x block_n macro tile, block_k deep, waves per workgroup,
- * group_m rows of tiles per L2 group (mma.py:22-30 GROUP_M). The 128x128x32 tile with 8 waves and
- * the 128x64x32 tile with 8 or 16 waves split each tile's K loop over 2 or 4 groups of 4 waves
- * (partial sums added through LDS inside the workgroup). */
+ * group_m rows of tiles per L2 group (mma.py:22-30 GROUP_M). The 128x128x32 and 64x64x32 tiles
+ * with 8 waves and the 128x64x32 tile with 8 or 16 waves split each tile's K loop over 2 or 4
+ * groups of 4 waves (partial sums added through LDS inside the workgroup). */
 typedef struct {
   int32_t block_m;
   int32_t block_n;

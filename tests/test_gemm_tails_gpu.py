@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 # every built tile (16x16 and 32x32 MFMAs; compiler-scheduled and pipelined loops)
 TILES = [(256, 256, 64, 8), (256, 256, 32, 8), (256, 128, 64, 8), (128, 256, 64, 8), (256, 256, 64, 4),
          (256, 256, 32, 4), (128, 128, 64, 4), (128, 128, 32, 4), (128, 64, 32, 4), (64, 256, 32, 4),
-         (128, 128, 32, 8), (128, 64, 32, 8), (128, 64, 32, 16)]
+         (128, 128, 32, 8), (128, 64, 32, 8), (128, 64, 32, 16), (64, 64, 32, 8)]
 # K from 1 to 32 slabs: up to 8 slabs the 128x128, 128x64 and 64x256 tiles launch their
 # shallow-ring kernels (K=256 is the last such for BK=32, K=264 the first deep one).
 SHAPES = [(100, 200, 72), (257, 260, 520), (33, 4, 8), (1000, 1004, 1000), (300, 512, 136), (260, 392, 256),
