@@ -479,6 +479,82 @@ def _bench_gemm_k256(torch, args, g, dev, vendor_rounds) -> dict:
     return gemm_k256_obj
 
 
+GEMM_SWEEP_SIZES = (1024, 2048, 4096, 16384)
+
+
+def _bench_gemm_sweep(torch, g, dev, rounds: int = 3) -> dict:
+    """The rest of the square GEMM sweep of BASELINE config 2 (8192^3 is the `gemm` object): each
+    size through the drop-in launcher and through torch.matmul (hipBLASLt), both timed as replays
+    of a HIP graph holding a batch of back-to-back launches (GPU time: an eager call of either
+    costs several microseconds of host time, more than a 1024^3 product takes), in alternating
+    rounds. A vendor graph whose replay does not reproduce the eager product (a library call may
+    record memset nodes) is timed eagerly instead, and says so."""
+    import mma
+
+    rows = []
+    for n in GEMM_SWEEP_SIZES:
+        a = (torch.rand(n, n, generator=g) * 2 - 1).half().to(dev)
+        b = (torch.rand(n, n, generator=g) * 2 - 1).half().to(dev)
+        c = torch.empty(n, n, dtype=torch.float16, device=dev)
+        c2 = torch.empty(n, n, dtype=torch.float16, device=dev)
+        bm, bn, bk, group_m, warps, stages = mma._select_2d_contiguous_config(n, n, n)
+        grid = (math.ceil(n / bm) * math.ceil(n / bn),)
+
+        def ours():
+            mma._matmul_contiguous_kernel[grid](a, b, c, n, n, n, BLOCK_M=bm, BLOCK_N=bn, BLOCK_K=bk,
+                                                GROUP_M=group_m, USE_CACHE_EVICTION_HINTS=True,
+                                                num_warps=warps, num_stages=stages)
+
+        def vendor():
+            torch.matmul(a, b, out=c2)
+
+        ours()
+        vendor()
+        torch.cuda.synchronize()
+        ref = a.float() @ b.float()
+        rel = ((c.float() - ref).norm() / ref.norm()).item()
+        eager_vendor = c2.clone()
+        del ref
+        batch = max(2, min(64, int(4e-3 / (2.0 * n ** 3 / 1.2e15))))  # ~4 ms of work per replay
+        graphs, protocol = {}, {}
+        for key, fn in (("ours", ours), ("vendor", vendor)):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for _ in range(batch):
+                    fn()
+            gr.replay()
+            torch.cuda.synchronize()
+            graphs[key] = gr.replay
+            protocol[key] = "graph"
+        if ((c2.float() - eager_vendor.float()).norm() / eager_vendor.float().norm()).item() > 1e-3:
+            graphs["vendor"] = lambda: [vendor() for _ in range(batch)]
+            protocol["vendor"] = "eager (its graph replay differed from the eager product)"
+        times = {k: [] for k in graphs}
+        for _ in range(rounds):
+            for key, run in graphs.items():
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                run()
+                e.record()
+                torch.cuda.synchronize()
+                times[key].append(s.elapsed_time(e) / batch)
+        us = {k: statistics.median(v) * 1e3 for k, v in times.items()}
+        flop = 2.0 * n ** 3
+        rows.append({"M": n, "N": n, "K": n, "us": round(us["ours"], 2),
+                     "tflops": round(flop / (us["ours"] * 1e-6) / 1e12, 1),
+                     "peak_frac": round(flop / (us["ours"] * 1e-6) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                     "tile": {"block_m": bm, "block_n": bn, "block_k": bk, "waves": warps, "group_m": group_m},
+                     "rel_fro": rel, "vendor_us": round(us["vendor"], 2),
+                     "speedup_vs_vendor": round(us["vendor"] / us["ours"], 3), "vendor_timing": protocol["vendor"]})
+        _log(f"gemm {n}^3: {rows[-1]['us']} us ({rows[-1]['tflops']} TFLOP/s), hipBLASLt {rows[-1]['vendor_us']} us "
+             f"({rows[-1]['speedup_vs_vendor']}x), rel_fro {rel:.2e}")
+        del a, b, c, c2, eager_vendor, graphs
+        torch.cuda.empty_cache()
+    return {"metric": "GEMM fp16 square sweep (BASELINE config 2), GPU time per launch",
+            "protocol": f"HIP-graph replays of batched back-to-back launches, {rounds} alternating rounds, median",
+            "vendor_library": "torch.matmul (hipBLASLt)", "rows": rows}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -644,6 +720,8 @@ def main() -> int:
     # 17.8 us at 8 TB/s); beside it, torch's fill of the same C (a pure 128 MiB write stream) on this GPU.
     # (not in counter runs: their summaries take each kernel's last dispatches as the 8192^3 launches)
     gemm_k256_obj = None if args.counter_run else _bench_gemm_k256(torch, args, g, dev, vendor_rounds)
+    # ---- the rest of config 2's square sweep, beside hipBLASLt in GPU time (not in counter or trace runs)
+    gemm_sweep_obj = None if (args.counter_run or args.no_vendor) else _bench_gemm_sweep(torch, g, dev)
 
     # ---- CPU baseline (reference CPU path, bounded sample) ---------------------------------------
     cpu_fa = cpu_gemm = None
@@ -715,6 +793,7 @@ def main() -> int:
             "vendor": gemm_vendor,
         },
         "gemm_k256": gemm_k256_obj,
+        "gemm_sweep": gemm_sweep_obj,
     }
     print(json.dumps(line), flush=True)
     return 0
