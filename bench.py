@@ -479,6 +479,87 @@ def _bench_gemm_k256(torch, args, g, dev, vendor_rounds) -> dict:
     return gemm_k256_obj
 
 
+# The rest of the attention sweeps of BASELINE configs 3 (fp16 B4 H32 D128, N 1024..16384, causal and
+# not; the headline is the non-causal N=8192 case) and 4 (bf16 B2 H16 D256 sliced, N 1024..8192).
+FA_SWEEP = ([dict(B=4, H=32, N=n, D=128, dtype="fp16", causal=c, variant="optimized", input_scale=1.0)
+             for n in (1024, 2048, 4096, 8192, 16384) for c in (False, True) if (n, c) != (8192, False)]
+            + [dict(B=2, H=16, N=n, D=256, dtype="bf16", causal=False, variant="sliced", input_scale=0.5)
+               for n in (1024, 2048, 4096, 8192)])
+
+
+def _bench_fa_sweep(torch, dev, rounds: int = 3) -> dict:
+    """Each FA_SWEEP case through its reference tuner class -> flash_attention (the tuned tile), timed
+    beside torch's scaled_dot_product_attention (its fused flash / memory-efficient backends; a case
+    neither backend takes gets no vendor figure) in alternating rounds of back-to-back launches, with
+    16 sampled output rows checked against fp32 math."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    import flash_atten
+    import tuner
+
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    rows_out = []
+    for cfg in FA_SWEEP:
+        B, H, N, D, causal = cfg["B"], cfg["H"], cfg["N"], cfg["D"], cfg["causal"]
+        dt = {"fp16": torch.float16, "bf16": torch.bfloat16}[cfg["dtype"]]
+        q, k, v = ((torch.randn(B, H, N, D, generator=gen, device=dev) * cfg["input_scale"]).to(dt) for _ in range(3))
+        tuner_cls = {"optimized": tuner.FlashAttentionOptimizeSharedMemTuner,
+                     "sliced": tuner.FlashAttentionBlockDNomaskTuner}[cfg["variant"]]
+        spec = tuner_cls(tuple(q.shape), tuple(k.shape), tuple(v.shape), q.element_size(), causal=causal,
+                         return_lse=False).build_flash_attention_launch_spec(q, k, v)
+        flops = 4.0 * B * H * D * (N * (N + 1) / 2 if causal else N * N)
+        ours = lambda: flash_atten.flash_attention(spec)
+        ours()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        ours()
+        e.record()
+        torch.cuda.synchronize()
+        per_round = max(2, min(32, int(4.0 / max(s.elapsed_time(e), 1e-3))))
+        fns = {"ours": ours}
+
+        def sdpa():
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+        try:
+            sdpa()
+            torch.cuda.synchronize()
+            fns["sdpa"] = sdpa
+        except RuntimeError:
+            pass
+        med = _alternating(torch, fns, rounds=rounds, per_round=per_round)
+        # 16 sampled rows against fp32 math
+        o = spec.kernel_args[3]
+        pick = torch.randint(0, B * H * N, (16,), generator=torch.Generator().manual_seed(N + D + causal))
+        bh, m = pick // N, pick % N
+        qs, ks, vs = (t.reshape(B * H, N, D)[idx].float() for t, idx in ((q, (bh, m)), (k, bh), (v, bh)))
+        sc = torch.bmm(ks, qs[:, :, None])[:, :, 0] * D ** -0.5
+        if causal:
+            sc = sc.masked_fill(torch.arange(N, device=dev)[None, :] > m.to(dev)[:, None], float("-inf"))
+        ref = torch.bmm(torch.softmax(sc, dim=-1)[:, None, :], vs)[:, 0, :]
+        err = (o.reshape(B * H, N, D)[bh, m].float() - ref).abs().max().item()
+        row = {"dtype": cfg["dtype"], "variant": cfg["variant"], "B": B, "H": H, "N": N, "D": D, "causal": causal,
+               "ms": round(med["ours"], 4), "tflops": round(flops / (med["ours"] * 1e-3) / 1e12, 1),
+               "peak_frac": round(flops / (med["ours"] * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+               "tile": {"block_m": spec.kernel_kwargs["BLOCK_M"], "block_n": spec.kernel_kwargs["BLOCK_N"],
+                        "waves": spec.kernel_kwargs["num_warps"], "stages": spec.kernel_kwargs["num_stages"]},
+               "max_abs_err_16_rows": err,
+               "vendor_ms": round(med["sdpa"], 4) if "sdpa" in med else None,
+               "speedup_vs_vendor": round(med["sdpa"] / med["ours"], 3) if "sdpa" in med else None}
+        rows_out.append(row)
+        _log(f"attention {cfg['dtype']} D{D} N{N} {'causal' if causal else 'non-causal'}: {row['ms']} ms "
+             f"({row['tflops']} TFLOP/s), SDPA {row['vendor_ms']} ms, max err {err:.2e}")
+        del q, k, v, spec, o, qs, ks, vs, sc, ref, fns
+        torch.cuda.empty_cache()
+    return {"metric": "FA forward sweeps of BASELINE configs 3 and 4 (the headline case is the main line)",
+            "protocol": f"{rounds} alternating rounds of back-to-back launches (~4 ms each), median per launch",
+            "vendor_library": "torch.nn.functional.scaled_dot_product_attention (flash / memory-efficient backends)",
+            "rows": rows_out}
+
+
 GEMM_SWEEP_SIZES = (1024, 2048, 4096, 16384)
 
 
@@ -722,6 +803,8 @@ def main() -> int:
     gemm_k256_obj = None if args.counter_run else _bench_gemm_k256(torch, args, g, dev, vendor_rounds)
     # ---- the rest of config 2's square sweep, beside hipBLASLt in GPU time (not in counter or trace runs)
     gemm_sweep_obj = None if (args.counter_run or args.no_vendor) else _bench_gemm_sweep(torch, g, dev)
+    # ---- the rest of configs 3 and 4's attention sweeps, beside torch SDPA (same runs skip it)
+    fa_sweep_obj = None if (args.counter_run or args.no_vendor) else _bench_fa_sweep(torch, dev)
 
     # ---- CPU baseline (reference CPU path, bounded sample) ---------------------------------------
     cpu_fa = cpu_gemm = None
@@ -794,6 +877,7 @@ def main() -> int:
         },
         "gemm_k256": gemm_k256_obj,
         "gemm_sweep": gemm_sweep_obj,
+        "fa_sweep": fa_sweep_obj,
     }
     print(json.dumps(line), flush=True)
     return 0
