@@ -610,12 +610,24 @@ struct Fwd16 {
         // wait for memory (the O stores then drain during step 1).
         if (prefetched) wait_vm_lds_barrier<63>();
         else wait_vm_lds_barrier<0>();
+        // Steps that take chunks of the next item's Q: 1 .. min(kQChunks, T) (none without a next
+        // item). The step loop tests this once and the tile ownership of K_{j+1} and V_j once: the
+        // per-chunk and per-operand tests it replaced, each a branch in every step, had made a step
+        // ~1-2% longer than the per-workgroup kernel's (same instructions otherwise).
+        const int q_last = __builtin_amdgcn_readfirstlane(nxt.ntiles > 0 ? min(kQChunks, ntiles) : 0);
         for (int j = 1; j <= ntiles; ++j) {
-          issue_k(j + 1);
-          issue_v(j);
+          if (__builtin_expect(j + 1 < ntiles, 1)) {  // K_{j+1} and V_j of this item
+            const uint32_t ks = kring_lds + (uint32_t)((par + j + 1) & 1) * (KT_ELEMS * 2) + wave * NKW * 1024;
+            buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + (uint32_t)(cur.t_begin + j + 1) * kstep, ks);
+            const uint32_t vs = vring_lds + (uint32_t)((par + j) & 1) * (VT_ELEMS * 2) + wave * NVW * 1024;
+            buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + (uint32_t)(cur.t_begin + j) * vstep, vs);
+          } else {
+            issue_k(j + 1);
+            issue_v(j);
+          }
           // every wave read its Q fragments before the barriers above: the buffer takes the next
           // item's Q, chunk c at step min(c + 1, T), so all of it has landed by the item's last wait
-          if (nxt.ntiles > 0) {
+          if (__builtin_expect(j <= q_last, 0)) {
 #pragma unroll
             for (int c = 0; c < kQChunks; ++c)
               if (j == min(c + 1, ntiles)) issue_q_chunk(nxt, c);
