@@ -61,6 +61,13 @@ DECODE = [
     # more splits than a wave has lanes: the merge takes split weights 64 at a time; 36 splits empty
     ("many_splits", 1, 8, 2, 1, 8192, 128, BF16, (128, 64, 4, 3), 100),
     ("many_splits_d256", 1, 4, 4, 2, 4000, 256, F16, (128, 32, 4, 3), 70),
+    # the 16x16x32 MFMA split kernels (stages 6-9; a stages=9 tile packing query heads runs stages 8)
+    ("m16_lean", 1, 32, 8, 1, 8192, 128, BF16, (128, 64, 4, 6), 64),
+    ("m16_pipelined_n32", 2, 32, 8, 1, 5000, 128, F16, (128, 32, 4, 7), 48),
+    ("m16_ping_pong", 1, 16, 2, 3, 3000, 128, BF16, (256, 64, 8, 8), 16),
+    ("m16_persistent_tile", 1, 32, 8, 1, 4096, 128, F16, (256, 64, 8, 9), 32),  # packs: runs stages 8
+    ("m16_d256_many_splits", 1, 8, 2, 1, 4000, 256, F16, (128, 32, 4, 6), 70),  # 64+ splits, 7 empty
+    ("m16_d64_unpacked", 2, 4, 4, 5, 2500, 64, BF16, (128, 64, 4, 7), 9),
 ]
 
 
@@ -139,3 +146,83 @@ def test_decode_step_replays_in_a_hip_graph(gpu):
         assert diff == 0.0, (rep, diff)
     o_ref, _ = oracle.attention(qd.float().cpu().numpy(), k, v, causal=False)
     assert max_abs(out.float().cpu().numpy(), o_ref) <= ATOL[BF16]
+
+
+def _garbage(nbytes, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, 256, (nbytes,), generator=g, dtype=torch.uint8).to("cuda:0")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("stages", [6, 7, 8])
+def test_split_workspace_needs_no_clearing(gpu, stages):
+    """A workspace of random bytes (never cleared), reused by calls with other split counts (so
+    each call's partials overlay another layout's), must give the oracle's result every time, and
+    a repeated call the same bits."""
+    B, H, Hkv, M, N, D, dtype = 2, 16, 4, 2, 4500, 128, F16
+    bm, bn, waves = (256, 64, 8) if stages == 8 else (128, 64, 4)
+    print(f"[decode] stale workspace reused across split counts, stages={stages}", flush=True)
+    q, k, v = make_qkv(606 + stages, B, H, Hkv, M, N, D, dtype)
+    qd, kd, vd = (to_device(x, dtype, "cuda:0") for x in (q, k, v))
+    o_ref, lse_ref = oracle.attention(q, k, v, causal=False)
+    ws = _garbage(max(hip_lib.workspace_bytes(B, H, M, D, s) for s in (24, 7, 70)), 31 + stages)
+    first = None
+    for splits in (24, 7, 70, 24):
+        o = torch.full_like(qd, float("nan"))
+        lse = torch.full((B, H, M), float("nan"), dtype=torch.float32, device="cuda:0")
+        hip_lib.fa_fwd(qd, kd, vd, o, lse, sm_scale=D ** -0.5, causal=False, variant=SLICED,
+                       tile=hip_lib.make_tile(bm, bn, waves, stages, splits), workspace=ws)
+        torch.cuda.synchronize()
+        on, ln = o.float().cpu().numpy(), lse.cpu().numpy()
+        assert np.isfinite(on).all() and np.isfinite(ln).all(), splits
+        assert max_abs(on, o_ref) <= ATOL[dtype], splits
+        assert max_abs(ln, lse_ref) <= 1e-3, splits
+        if splits == 24:
+            if first is None:
+                first = (on, ln)
+            else:
+                assert np.array_equal(on, first[0]) and np.array_equal(ln, first[1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("stages", [6, 8])
+def test_split_workspace_shared_by_graph_and_eager_calls(gpu, stages):
+    """One workspace serves a captured decode step and eager calls in turn: replays right after an
+    eager call and back-to-back replays must both match the eager result bit for bit, with the
+    query changed in place between rounds."""
+    B, H, Hkv, M, N, D, dtype, splits = 1, 32, 8, 1, 6000, 128, BF16, 40
+    bm, bn, waves = (256, 64, 8) if stages == 8 else (128, 64, 4)
+    print(f"[decode] graph and eager calls on one workspace, stages={stages}", flush=True)
+    q, k, v = make_qkv(7070 + stages, B, H, Hkv, M, N, D, dtype)
+    qd, kd, vd = (to_device(x, dtype, "cuda:0") for x in (q, k, v))
+    ws = _garbage(hip_lib.workspace_bytes(B, H, M, D, splits), 5)
+    tile = hip_lib.make_tile(bm, bn, waves, stages, splits)
+    o_g, o_e = torch.empty_like(qd), torch.empty_like(qd)
+    lse_g = torch.empty((B, H, M), dtype=torch.float32, device="cuda:0")
+    lse_e = torch.empty_like(lse_g)
+
+    def call(o, lse):
+        hip_lib.fa_fwd(qd, kd, vd, o, lse, sm_scale=D ** -0.5, causal=False, variant=SLICED, tile=tile,
+                       workspace=ws)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(o_g, lse_g)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(o_g, lse_g)
+    g = torch.Generator().manual_seed(6)
+    for rep in range(3):
+        qd.copy_(torch.randn(qd.shape, generator=g).to(dtype))
+        call(o_e, lse_e)
+        torch.cuda.synchronize()
+        for back_to_back in range(2):
+            o_g.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(o_g, o_e) and torch.equal(lse_g, lse_e), (rep, back_to_back)
+    o_ref, lse_ref = oracle.attention(qd.float().cpu().numpy(), k, v, causal=False)
+    assert max_abs(o_g.float().cpu().numpy(), o_ref) <= ATOL[dtype]
+    assert max_abs(lse_g.cpu().numpy(), lse_ref) <= 1e-3
