@@ -206,6 +206,29 @@ def test_fa_sliced_pipelined_split_kv(gpu, splits, causal):
         assert max_abs(lse, lse_ref) <= 1e-3, tile_name
 
 
+@pytest.mark.parametrize("stages", [8, 9])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fa_ping_pong_offset_moves(gpu, stages, causal):
+    """Large and climbing logits through the ping-pong kernels, whose lazy rescale moves a row's
+    exponent offset only when a score rises more than 8 (log2 units) above it. Keys whose norm grows
+    along the sequence make every row's maximum climb tile after tile (many moves), and a large scale
+    puts the logits at tens of units; a causal launch adds rows whose first tiles are masked. The
+    logits are formed in fp32 from the binary16 inputs, so the LSE error stays at the fp32 level
+    relative to its magnitude (a variant that folded the scale into Q, rounded to binary16, was
+    8x less accurate at |LSE| ~ 70 and is not used)."""
+    B, H, Hkv, M, N, D, dtype = 1, 4, 2, 512, 1536, 128, F16
+    print(f"[fa_abi] ping-pong offset moves stages={stages} causal={causal}", flush=True)
+    q, k, v = make_qkv(91, B, H, Hkv, M, N, D, dtype)
+    ramp = np.linspace(0.25, 2.5, N, dtype=np.float32)[None, None, :, None]
+    k = oracle.round_to(k * ramp, oracle.DTYPE_F16)
+    for scale in (None, 0.6):
+        o, lse = run_fa(q, k, v, variant=OPT, tile=(OPT, 256, 64, 8, stages), causal=causal, dtype=dtype, scale=scale)
+        o_ref, lse_ref = oracle.attention(q, k, v, causal=causal, scale=scale)
+        assert np.isfinite(o).all() and np.isfinite(lse).all(), scale
+        assert max_abs(o, o_ref) <= ATOL[dtype], scale
+        assert max_abs(lse, lse_ref) <= 1e-3 * max(1.0, float(np.abs(lse_ref).max()) / 8), scale
+
+
 # Persistent grid (stages=9) with several work items per workgroup (more query blocks than CUs):
 # name, B, H, Hkv, M, N, D, dtype, causal, splits
 PERSISTENT_CASES = [
