@@ -23,6 +23,7 @@ import math
 import os
 import statistics
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -74,6 +75,78 @@ def _clock_warmup(torch, fn, ms: float) -> int:
         done += n
         n = min(2 * n, 64)
     return done
+
+
+class ClockSampler:
+    """The graphics clock of this process's GPU under a given load: amdsmi's GPU metrics (the
+    XCDs' current gfx clocks, averaged), matched to torch's device by PCI bus. The firmware
+    refreshes those metrics about once a second (a 1 s GEMM burst saw one change, from idle to
+    1.67-1.77 GHz), so measure() runs the launch back to back for a few seconds and averages the
+    readings of the burst's second half. Reading only; None where amdsmi, the device match or the
+    metric is unavailable (the bench then reports no clock)."""
+
+    def __init__(self, torch, dev):
+        self.amdsmi = self.handle = None
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            props = torch.cuda.get_device_properties(dev)
+            bus, domain = getattr(props, "pci_bus_id", None), getattr(props, "pci_domain_id", 0)
+            if bus is None:
+                return
+            for h in amdsmi.amdsmi_get_processor_handles():
+                bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)  # "dddd:bb:dd.f"
+                dom, b = (int(x, 16) for x in bdf.split(":")[:2])
+                if b == bus and dom == domain:
+                    self.amdsmi, self.handle = amdsmi, h
+                    break
+            if self.handle is not None and self._read() is None:
+                self.handle = None
+        except Exception:  # no amdsmi, no permission, no such metric: no clock in the line
+            self.handle = None
+
+    def _read(self) -> float | None:
+        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.handle)
+        vals = [x for x in (m.get("current_gfxclks") or []) if isinstance(x, (int, float)) and 0 < x < 10000]
+        if not vals and isinstance(m.get("current_gfxclk"), (int, float)) and 0 < m["current_gfxclk"] < 10000:
+            vals = [m["current_gfxclk"]]
+        return sum(vals) / len(vals) if vals else None
+
+    def measure(self, torch, fn, seconds: float = 2.5) -> float | None:
+        """Mean clock (GHz) while `fn` runs back to back for `seconds` (batches of ~20 ms)."""
+        if self.handle is None:
+            return None
+        samples: list[tuple[float, float]] = []
+        stop = threading.Event()
+        t0 = time.perf_counter()
+
+        def loop():
+            while not stop.is_set():
+                try:
+                    v = self._read()
+                except Exception:
+                    v = None
+                if v:
+                    samples.append((time.perf_counter() - t0, v))
+                stop.wait(0.01)
+
+        thread = threading.Thread(target=loop, daemon=True)
+        thread.start()
+        n = 1
+        try:
+            while time.perf_counter() - t0 < seconds:
+                b0 = time.perf_counter()
+                for _ in range(n):
+                    fn()
+                torch.cuda.synchronize()
+                if time.perf_counter() - b0 < 0.02:
+                    n = min(2 * n, 256)
+        finally:
+            stop.set()
+            thread.join()
+        late = [v for t, v in samples if t >= seconds / 2]
+        return round(statistics.mean(late) / 1000.0, 3) if late else None
 
 
 def _time_launches(torch, fn, steps: int, warmup: int, clock_warmup_ms: float = 0.0):
@@ -724,6 +797,9 @@ def main() -> int:
          f"waves={spec.kernel_kwargs['num_warps']} stages={spec.kernel_kwargs['num_stages']}")
     total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup,
                                    args.clock_warmup_ms)
+    # the clock under the same launches, after the timed ones (none beside counter passes)
+    clock = ClockSampler(torch, dev) if not args.counter_run else None
+    fa_clock = clock.measure(torch, lambda: flash_atten.flash_attention(spec)) if clock else None
     fa_launch_ms = statistics.mean(per)
     fa_tflops_launch = fa_flops / (fa_launch_ms * 1e-3) / 1e12
     fa_ms_per_step = total_ms / args.steps
@@ -775,6 +851,7 @@ def main() -> int:
                                             USE_CACHE_EVICTION_HINTS=True, num_warps=warps, num_stages=stages)
 
     g_total, g_per = _time_launches(torch, gemm, args.steps, args.warmup, args.clock_warmup_ms)
+    gemm_clock = clock.measure(torch, gemm) if clock else None
     gemm_flops = 2.0 * M * Ng * K
     gemm_launch_ms = statistics.mean(g_per)
     gemm_tflops = gemm_flops / (g_total / args.steps * 1e-3) / 1e12
@@ -787,6 +864,7 @@ def main() -> int:
         med = _alternating(torch, {"ours": gemm, "hipblaslt": lambda: torch.matmul(a, b, out=c)},
                            rounds=vendor_rounds[0], per_round=vendor_rounds[1])
         gemm_vendor = {"library": "torch.matmul (hipBLASLt)",
+                       "clock_ghz": clock.measure(torch, lambda: torch.matmul(a, b, out=c)) if clock else None,
                        "value": round(gemm_flops / (med["hipblaslt"] * 1e-3) / 1e12, 2),
                        "ours_same_rounds": round(gemm_flops / (med["ours"] * 1e-3) / 1e12, 2),
                        "speedup": round(med["hipblaslt"] / med["ours"], 3),
@@ -840,6 +918,7 @@ def main() -> int:
                                 f"sm_scale=1/sqrt(D)"),
                    "B": B, "H": H, "N": N, "D": D, "causal": causal},
         "mfma_peak_frac": round(fa_tflops / PEAK_FP16_TFLOPS, 4),
+        "clock_ghz": fa_clock,
         "roofline": {
             "bound": "mfma",
             "achieved": round(fa_tflops_launch, 2),
@@ -860,6 +939,7 @@ def main() -> int:
             "value": round(gemm_tflops, 2),
             "ms_per_step": round(g_total / args.steps, 4),
             "tile": {"block_m": bm, "block_n": bn, "block_k": bk, "waves": warps, "group_m": group_m},
+            "clock_ghz": gemm_clock,
             "roofline": {
                 "bound": "mfma",
                 "achieved": round(gemm_flops / (gemm_launch_ms * 1e-3) / 1e12, 2),
