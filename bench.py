@@ -725,6 +725,9 @@ def main() -> int:
                     help="attention tile as the reference's tune arguments (BLOCK_M, BLOCK_N, NUM_WARPS, "
                          "NUM_STAGES) instead of the tuning table's choice")
     ap.add_argument("--no-vendor", action="store_true", help="skip the alternating vendor-library timings")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the clock bursts after the timed launches (kernel-trace runs: the trace's last "
+                         "launches of each kernel are then the timed ones)")
     ap.add_argument("--clock-warmup-ms", type=float, default=200.0,
                     help="GPU time of back-to-back launches before each kernel's warm-up launches, so the timed "
                          "launches run at the steady clock (0 disables)")
@@ -798,7 +801,7 @@ def main() -> int:
     total_ms, per = _time_launches(torch, lambda: flash_atten.flash_attention(spec), args.steps, args.warmup,
                                    args.clock_warmup_ms)
     # the clock under the same launches, after the timed ones (none beside counter passes)
-    clock = ClockSampler(torch, dev) if not args.counter_run else None
+    clock = ClockSampler(torch, dev) if not (args.counter_run or args.no_clock) else None
     fa_clock = clock.measure(torch, lambda: flash_atten.flash_attention(spec)) if clock else None
     fa_launch_ms = statistics.mean(per)
     fa_tflops_launch = fa_flops / (fa_launch_ms * 1e-3) / 1e12
