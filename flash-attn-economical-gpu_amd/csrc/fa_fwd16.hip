@@ -166,41 +166,77 @@ struct Fwd16 {
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[dt][qt][r] *= alpha;
   }
-  // Lazy rescale: move the exponent offset m_use (and rescale O and l) only when some lane of the
-  // wave sees a score more than THRESH (log2 units) above it; the moved offset is the row max over
-  // the four lane rows, so the lanes of a query keep one offset.
-  __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, float (&m_use)[QT], float (&l_i)[QT],
+  // Exponent offsets of a wave's QT query tiles: m in score units (-inf before the first tile),
+  // and two values derived from it: mc(c) = m c (0 while m is -inf), the offset every score's FMA
+  // subtracts, and thr(c) = m + THRESH / c, the bound of the rescale test. The ping-pong kernels,
+  // whose softmax phase is VALU-bound, keep both and update them only when the offset moves
+  // (rare; measured 0.4-0.7% faster non-causal); the others take them per step (the 256-dimension
+  // kernel at its register cap ran 4.5% slower keeping them).
+  static constexpr bool kCachedOff = PIPE >= 2;
+  struct RowOff {
+    float m[QT], mc_[kCachedOff ? QT : 1], thr_[kCachedOff ? QT : 1];
+    __device__ inline void reset() {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = FA_NEG_INF;
+        if constexpr (kCachedOff) {
+          mc_[qt] = 0.f;
+          thr_[qt] = FA_NEG_INF;
+        }
+      }
+    }
+    __device__ inline void set(int qt, float m_new, float c) {
+      m[qt] = m_new;
+      if constexpr (kCachedOff) {
+        mc_[qt] = (m_new == FA_NEG_INF) ? 0.f : m_new * c;
+        thr_[qt] = m_new + THRESH / c;
+      }
+    }
+    __device__ inline float mc(int qt, float c) const {
+      if constexpr (kCachedOff) return mc_[qt];
+      else return (m[qt] == FA_NEG_INF) ? 0.f : m[qt] * c;
+    }
+    __device__ inline float thr(int qt, float c) const {
+      if constexpr (kCachedOff) return thr_[qt];
+      else return m[qt] + THRESH / c;
+    }
+  };
+
+  // Lazy rescale: move the exponent offset (and rescale O and l) only when some lane of the wave
+  // sees a score more than THRESH (log2 units) above it; the moved offset is the row max over the
+  // four lane rows, so the lanes of a query keep one offset.
+  __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, RowOff& ro, float (&l_i)[QT],
                                         floatx4 (&lsum)[QT], float c) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const bool need = mx[qt] > m_use[qt] + THRESH / c;
+      const bool need = mx[qt] > ro.thr(qt, c);
       if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        const float m_new = fmaxf(m_use[qt], xquad_max(mx[qt]));
-        const float alpha = (m_use[qt] == FA_NEG_INF) ? 0.f : fast_exp2((m_use[qt] - m_new) * c);
-        m_use[qt] = m_new;
+        const float m_new = fmaxf(ro.m[qt], xquad_max(mx[qt]));
+        const float alpha = (ro.m[qt] == FA_NEG_INF) ? 0.f : fast_exp2((ro.m[qt] - m_new) * c);
+        ro.set(qt, m_new, c);
         scale_row(qt, alpha, acc, l_i, lsum);
       }
     }
   }
 
   // Online softmax of one score tile: masks where needed, row max, lazy rescale, then P.
-  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][QT], OAcc& acc, float (&m_use)[QT],
+  __device__ static inline void softmax(STile& s, u32x4 (&pk)[KC][QT], OAcc& acc, RowOff& ro,
                                         float (&l_i)[QT], floatx4 (&lsum)[QT], int n0, int wrow0, int q16, int g,
                                         const FwdParams& p) {
     if (tile_needs_mask(n0, wrow0, p)) mask_tile(s, n0, wrow0, q16, g, p);
     float mx[QT];
     tile_max(s, mx);
-    rescale(mx, acc, m_use, l_i, lsum, p.c);
-    exp_pack(s, pk, m_use, l_i, p.c);
+    rescale(mx, acc, ro, l_i, lsum, p.c);
+    exp_pack(s, pk, ro, l_i, p.c);
   }
 
-  // P = exp2(S c - m_use c) rounded to the input dtype and packed as the B operand of P V; the row
+  // P = exp2(S c - m c) rounded to the input dtype and packed as the B operand of P V; the row
   // sum l accumulates the same P.
-  __device__ static inline void exp_pack(const STile& s, u32x4 (&pk)[KC][QT], const float (&m_use)[QT],
+  __device__ static inline void exp_pack(const STile& s, u32x4 (&pk)[KC][QT], const RowOff& ro,
                                          float (&l_i)[QT], float c) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const float mc = (m_use[qt] == FA_NEG_INF) ? 0.f : m_use[qt] * c;
+      const float mc = ro.mc(qt, c);
       float l0 = 0.f, l1 = 0.f;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
@@ -292,7 +328,7 @@ struct Fwd16 {
   // kernel past its 168-VGPR cap into scratch). l over the four lane rows, O = acc / l; lane holds
   // d = 16 dt + 4 g .. +3. The output parameters are read from the kernel-argument segment (scalar
   // loads at the point of use); fa_fwd16_kernel takes FwdParams as its only argument (checked there).
-  __device__ __attribute__((always_inline)) static inline void store_out(const OAcc& acc, const float (&m_use)[QT], const float (&l_i)[QT],
+  __device__ __attribute__((always_inline)) static inline void store_out(const OAcc& acc, const RowOff& ro, const float (&l_i)[QT],
                                           const floatx4 (&lsum)[QT], int wrow0, int q16, int g, int rows, int b, int h,
                                           int split_u) {
     const auto pe = kernarg_params<FwdParams>();
@@ -302,7 +338,7 @@ struct Fwd16 {
       const float l = kSumMfma ? lsum[qt][0] : xquad_sum(l_i[qt]);
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
-      const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      const float lse_val = (l > 0.f) ? (ro.m[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
       u32x4 wide[DTL / 2];
       if constexpr (kWideO) pack_o_wide(acc, qt, inv, wide);  // cross-lane: before the row test
       if (i < rows) {
@@ -548,11 +584,12 @@ struct Fwd16 {
       auto vslot = [&](int u) { return vlane + ((par + u) & 1) * VT_ELEMS; };
 
       OAcc acc;
-      float m_use[QT], l_i[QT];
+      RowOff ro;
+      ro.reset();
+      float l_i[QT];
       floatx4 lsum[QT];
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        m_use[qt] = FA_NEG_INF;
         l_i[qt] = 0.f;
         lsum[qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -589,7 +626,7 @@ struct Fwd16 {
           __builtin_amdgcn_s_setprio(0);
         };
         auto softmax_block = [&](int t) {
-          if (t < ntiles) softmax(s, pk, acc, m_use, l_i, lsum, (cur.t_begin + t) * BN, wrow0, q16, g, p);
+          if (t < ntiles) softmax(s, pk, acc, ro, l_i, lsum, (cur.t_begin + t) * BN, wrow0, q16, g, p);
         };
         if (GRP == 0 && wave_has_rows) {
           qk(s, qf, kslot(0));
@@ -647,7 +684,7 @@ struct Fwd16 {
       {
         const auto pe = kernarg_params<FwdParams>();
         const Ids ids = decode(cur.pid, *pe);
-        store_out(acc, m_use, l_i, lsum, wrow0, q16, g, pe->M, ids.b, ids.h, ids.split);
+        store_out(acc, ro, l_i, lsum, wrow0, q16, g, pe->M, ids.b, ids.h, ids.split);
       }
       if (pid_n < 0) break;
       prefetched = ntiles > 0 && nxt.ntiles > 0;
@@ -734,11 +771,12 @@ struct Fwd16 {
     const int ntiles = t_end > t_begin ? t_end - t_begin : 0;
 
     OAcc acc;
-    float m_use[QT], l_i[QT];
+    RowOff ro;
+    ro.reset();
+    float l_i[QT];
     floatx4 lsum[QT];  // row sums of the ones-row MFMA (kSumMfma)
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      m_use[qt] = FA_NEG_INF;
       l_i[qt] = 0.f;
       lsum[qt] = (floatx4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -808,7 +846,7 @@ struct Fwd16 {
         __builtin_amdgcn_s_setprio(0);
       };
       auto softmax_block = [&](int t) {
-        if (t < ntiles) softmax(s, pk, acc, m_use, l_i, lsum, (t_begin + t) * BN, wrow0, q16, g, p);
+        if (t < ntiles) softmax(s, pk, acc, ro, l_i, lsum, (t_begin + t) * BN, wrow0, q16, g, p);
       };
       // Group G's sequence; phases 2j and 2j+1 form iteration j. The branches on G and on
       // wave_has_rows are wave-uniform, and every wave runs the same barriers.
@@ -882,9 +920,9 @@ struct Fwd16 {
         issue_v(u + 1);
         if (wave_has_rows) {  // waves without rows still move their share of K/V
           fix_masked(cur, mx_cur, u);
-          rescale(mx_cur, acc, m_use, l_i, lsum, p.c);
+          rescale(mx_cur, acc, ro, l_i, lsum, p.c);
           u32x4 pk[KC][QT];
-          exp_pack(cur, pk, m_use, l_i, p.c);
+          exp_pack(cur, pk, ro, l_i, p.c);
           qk(nxt, qf, klane + ((u + 1) & 1) * KT_ELEMS);
           x_schedule();
           pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
@@ -896,9 +934,9 @@ struct Fwd16 {
       auto last = [&](STile& cur, float (&mx_cur)[QT], int u) {
         if (!wave_has_rows) return;
         fix_masked(cur, mx_cur, u);
-        rescale(mx_cur, acc, m_use, l_i, lsum, p.c);
+        rescale(mx_cur, acc, ro, l_i, lsum, p.c);
         u32x4 pk[KC][QT];
-        exp_pack(cur, pk, m_use, l_i, p.c);
+        exp_pack(cur, pk, ro, l_i, p.c);
         pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
         pv_schedule();
       };
@@ -931,7 +969,7 @@ struct Fwd16 {
         u32x4 pk[KC][QT];
         qk(s, qf, klane + (u & 1) * KT_ELEMS);
         qk_schedule();
-        softmax(s, pk, acc, m_use, l_i, lsum, (t_begin + u) * BN, wrow0, q16, g, p);
+        softmax(s, pk, acc, ro, l_i, lsum, (t_begin + u) * BN, wrow0, q16, g, p);
         pv(acc, pk, vlane + (u & 1) * VT_ELEMS, lsum);
         pv_schedule();
       }
@@ -950,7 +988,7 @@ struct Fwd16 {
       const float l = kSumMfma ? lsum[qt][0] : xquad_sum(l_i[qt]);
       const int i = wrow0 + qt * 16 + q16;
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
-      const float lse_val = (l > 0.f) ? (m_use[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
+      const float lse_val = (l > 0.f) ? (ro.m[qt] * pe->c + __builtin_amdgcn_logf(l)) * kLn2 : FA_NEG_INF;
       u32x4 wide[DTL / 2];
       if constexpr (kWideO) pack_o_wide(acc, qt, inv, wide);  // cross-lane: before the row test
       if (i < rows) {
