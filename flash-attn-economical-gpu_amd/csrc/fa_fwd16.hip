@@ -141,14 +141,18 @@ struct Fwd16 {
   }
 
   // Max of a score tile over this lane's keys of each query (a quarter of the row: the row's max
-  // over the four lane rows is formed only when the offset moves, in rescale).
+  // over the four lane rows is formed only when the offset moves, in rescale). A chain that takes
+  // two scores per step (v_max3_f32): 4·JT/2 ops per query tile, where a tree per key tile costs more.
   __device__ static inline void tile_max(const STile& s, float (&mx)[QT]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float m = FA_NEG_INF;
+      float m = fmaxf(s[0][qt][0], s[0][qt][1]);
+      m = fmaxf(fmaxf(m, s[0][qt][2]), s[0][qt][3]);
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt)
-        m = fmaxf(m, fmaxf(fmaxf(s[jt][qt][0], s[jt][qt][1]), fmaxf(s[jt][qt][2], s[jt][qt][3])));
+      for (int jt = 1; jt < JT; ++jt) {
+        m = fmaxf(fmaxf(m, s[jt][qt][0]), s[jt][qt][1]);
+        m = fmaxf(fmaxf(m, s[jt][qt][2]), s[jt][qt][3]);
+      }
       mx[qt] = m;
     }
   }
