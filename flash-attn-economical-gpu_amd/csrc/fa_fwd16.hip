@@ -208,13 +208,20 @@ struct Fwd16 {
 
   // Lazy rescale: move the exponent offset (and rescale O and l) only when some lane of the wave
   // sees a score more than THRESH (log2 units) above it; the moved offset is the row max over the
-  // four lane rows, so the lanes of a query keep one offset.
+  // four lane rows, so the lanes of a query keep one offset. One ballot over all query tiles guards
+  // the per-tile tests, so a step that moves no offset (the common case) takes a single branch.
   __device__ static inline void rescale(const float (&mx)[QT], OAcc& acc, RowOff& ro, float (&l_i)[QT],
                                         floatx4 (&lsum)[QT], float c) {
+    bool need[QT], any = false;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const bool need = mx[qt] > ro.thr(qt, c);
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      need[qt] = mx[qt] > ro.thr(qt, c);
+      any |= need[qt];
+    }
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(any) == 0, 1)) return;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      if (__builtin_amdgcn_ballot_w64(need[qt]) != 0) {
         const float m_new = fmaxf(ro.m[qt], xquad_max(mx[qt]));
         const float alpha = (ro.m[qt] == FA_NEG_INF) ? 0.f : fast_exp2((ro.m[qt] - m_new) * c);
         ro.set(qt, m_new, c);
