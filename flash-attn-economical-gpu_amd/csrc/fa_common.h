@@ -162,6 +162,20 @@ __device__ inline u32x4 make_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
+// The resource of make_rsrc moved `shift` bytes on (shift <= its range: the range shrinks by as
+// much, so a load at offset o of the result reads zeros exactly where o + shift did in `r`), or
+// with range 0 (every load reads zeros) when !live. Scalar arithmetic only: r, shift and live are
+// uniform.
+__device__ inline u32x4 slab_rsrc(const u32x4& r, uint32_t shift, bool live) {
+  const uint64_t a = (((uint64_t)r[1] << 32) | r[0]) + shift;  // base < 2^48: no carry into the stride
+  u32x4 s;
+  s[0] = (uint32_t)a;
+  s[1] = (uint32_t)(a >> 32);
+  s[2] = live ? r[2] - shift : 0u;
+  s[3] = r[3];
+  return s;
+}
+
 // 16 bytes per lane from the buffer straight into LDS (buffer_load_dwordx4 ... lds): lane i writes
 // lds_block[16 i .. 16 i + 15], so one wave instruction fills one contiguous 1 KiB block (M0 holds
 // the wave-uniform block address). Completion is tracked by vmcnt. The instruction is issued from

@@ -486,24 +486,29 @@ struct GemmKernel {
         const uint32_t slot = ring_lds + (uint32_t)(ks % RING) * SLAB_BYTES;
         const int gk = kbase + ks;
         const bool live = (ks < per) & (gk < ksteps);
-        // The slab's offset is a scalar added to the lane's: past the last slab that scalar is 2^31,
-        // beyond every range (operand spans stay below 2 GiB: the host checks), so the slot reads
-        // zeros with one vector add per instruction. Only the last slab of a K that is not a
-        // multiple of BK checks its columns per lane, in a uniform branch (16x16 tiles: 8192^3
-        // 2.4% faster; the 4-wave 32x32 tiles, at 256 VGPRs, spilled with the branch and keep one
-        // select per lane).
+        // 16x16 tiles: the slab's offset moves the buffer resource (base + offset, range - offset,
+        // range 0 past the last slab), so each lane's offset is the same on every step and the
+        // DMA takes no vector op; a lane reads zeros exactly where it did with the offset added to
+        // its own. Only the last slab of a K that is not a multiple of BK checks its columns per
+        // lane, in a uniform branch, with an offset of 2^31, past every range (operand spans stay
+        // below 2 GiB: the host checks). The 4-wave 32x32 tiles, at 256 VGPRs, add the slab
+        // offset (2^31 past the last slab) to the lane's and keep one select per lane for A.
         if constexpr (j < A_PER_WAVE && MI == 16) {
-          const uint32_t sbase = live ? (uint32_t)gk * a_slab_bytes : 0x80000000u;
-          uint32_t off = aoffs[j] + sbase;
+          uint32_t off = aoffs[j];
           if (__builtin_expect(k_ragged && gk == ksteps - 1, 0)) {
             if (gk * BK + ak0[j] >= p.K) off = 0x80000000u;
           }
-          buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
+          buffer_load16_to_lds(slab_rsrc(ars, (uint32_t)gk * a_slab_bytes, live), off,
+                               slot + (wave_u * A_PER_WAVE + j) * 1024);
         } else if constexpr (j < A_PER_WAVE) {
           // bitwise, not short-circuit: the scalar and per-lane parts stay one select
           const bool zero = !live | (k_ragged & (gk == ksteps - 1) & (gk * BK + ak0[j] >= p.K));
           const uint32_t off = zero ? 0x80000000u : aoffs[j] + (uint32_t)gk * a_slab_bytes;
           buffer_load16_to_lds(ars, off, slot + (wave_u * A_PER_WAVE + j) * 1024);
+        } else if constexpr (MI == 16) {
+          constexpr int jb = j - A_PER_WAVE;
+          buffer_load16_to_lds(slab_rsrc(brs, (uint32_t)gk * b_slab_bytes, live), boffs[jb],
+                               slot + A_BYTES + (wave_u * B_PER_WAVE + jb) * 1024);
         } else {
           constexpr int jb = j - A_PER_WAVE;
           const uint32_t off = boffs[jb] + (live ? (uint32_t)gk * b_slab_bytes : 0x80000000u);
