@@ -516,7 +516,8 @@ struct Fwd16 {
     const uint16_t* vlane = vring + lane * 4;
     const uint16_t* qlane = qbuf + (wave * QT * DC) * 512 + lane * 8;
 
-    // bytes between consecutive KV tiles of K and of V (the host keeps them below 2^32)
+    // bytes between consecutive KV tiles of K and of V (the host keeps them below 2^32); a tile's
+    // offset moves the buffer resource (slab_rsrc), so the lanes' offsets koff / voff stay fixed
     const uint32_t kstep = (uint32_t)BN * (uint32_t)p.sk2 * 2u, vstep = (uint32_t)BN * (uint32_t)p.sv2 * 2u;
     // Item-level parameters (pointers, strides, grid shape) are read through a fresh kernel-
     // argument pointer at each item boundary rather than held in scalar registers across the KV
@@ -548,23 +549,23 @@ struct Fwd16 {
       auto issue_k = [&](int u) {
         const uint32_t slot = kring_lds + (uint32_t)((par + u) & 1) * (KT_ELEMS * 2) + wave * NKW * 1024;
         if (__builtin_expect(u < ntiles, 1)) {
-          buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + (uint32_t)(cur.t_begin + u) * kstep, slot);
+          buffer_load16_to_lds_blocks<NKW, 64>(slab_rsrc(krs, (uint32_t)(cur.t_begin + u) * kstep, true), koff, slot);
         } else if (u - ntiles < nxt.ntiles) {
           asm volatile("");
           const uint32_t toff = (uint32_t)(nxt.t_begin + u - ntiles) * kstep;
           const auto pn = kernarg_params<FwdParams>();
-          buffer_load16_to_lds_blocks<NKW, 64>(k_rsrc(decode(nxt.pid, *pn), *pn), koff + toff, slot);
+          buffer_load16_to_lds_blocks<NKW, 64>(slab_rsrc(k_rsrc(decode(nxt.pid, *pn), *pn), toff, true), koff, slot);
         }
       };
       auto issue_v = [&](int u) {
         const uint32_t slot = vring_lds + (uint32_t)((par + u) & 1) * (VT_ELEMS * 2) + wave * NVW * 1024;
         if (__builtin_expect(u < ntiles, 1)) {
-          buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + (uint32_t)(cur.t_begin + u) * vstep, slot);
+          buffer_load16_to_lds_blocks<NVW, 32>(slab_rsrc(vrs, (uint32_t)(cur.t_begin + u) * vstep, true), voff, slot);
         } else if (u - ntiles < nxt.ntiles) {
           asm volatile("");
           const uint32_t toff = (uint32_t)(nxt.t_begin + u - ntiles) * vstep;
           const auto pn = kernarg_params<FwdParams>();
-          buffer_load16_to_lds_blocks<NVW, 32>(v_rsrc(decode(nxt.pid, *pn), *pn), voff + toff, slot);
+          buffer_load16_to_lds_blocks<NVW, 32>(slab_rsrc(v_rsrc(decode(nxt.pid, *pn), *pn), toff, true), voff, slot);
         }
       };
       auto issue_q = [&](const Item& it) {
@@ -666,9 +667,9 @@ struct Fwd16 {
         for (int j = 1; j <= ntiles; ++j) {
           if (__builtin_expect(j + 1 < ntiles, 1)) {  // K_{j+1} and V_j of this item
             const uint32_t ks = kring_lds + (uint32_t)((par + j + 1) & 1) * (KT_ELEMS * 2) + wave * NKW * 1024;
-            buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + (uint32_t)(cur.t_begin + j + 1) * kstep, ks);
+            buffer_load16_to_lds_blocks<NKW, 64>(slab_rsrc(krs, (uint32_t)(cur.t_begin + j + 1) * kstep, true), koff, ks);
             const uint32_t vs = vring_lds + (uint32_t)((par + j) & 1) * (VT_ELEMS * 2) + wave * NVW * 1024;
-            buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + (uint32_t)(cur.t_begin + j) * vstep, vs);
+            buffer_load16_to_lds_blocks<NVW, 32>(slab_rsrc(vrs, (uint32_t)(cur.t_begin + j) * vstep, true), voff, vs);
           } else {
             issue_k(j + 1);
             issue_v(j);
@@ -822,13 +823,20 @@ struct Fwd16 {
       if (u >= ntiles) return;
       const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sk2 * 2u;
       const uint32_t slot = kring_lds + (uint32_t)(u & 1) * (KT_ELEMS * 2);
-      buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + toff, slot + wave * NKW * 1024);
+      // uniform tile offset (64-key kernels): it moves the resource, the lanes' offsets stay fixed
+      if constexpr (kScalarIds)
+        buffer_load16_to_lds_blocks<NKW, 64>(slab_rsrc(krs, toff, true), koff, slot + wave * NKW * 1024);
+      else
+        buffer_load16_to_lds_blocks<NKW, 64>(krs, koff + toff, slot + wave * NKW * 1024);
     };
     auto issue_v = [&](int u) {
       if (u >= ntiles) return;
       const uint32_t toff = (uint32_t)((t_begin + u) * BN) * (uint32_t)p.sv2 * 2u;
       const uint32_t slot = vring_lds + (uint32_t)(u & 1) * (VT_ELEMS * 2);
-      buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + toff, slot + wave * NVW * 1024);
+      if constexpr (kScalarIds)
+        buffer_load16_to_lds_blocks<NVW, 32>(slab_rsrc(vrs, toff, true), voff, slot + wave * NVW * 1024);
+      else
+        buffer_load16_to_lds_blocks<NVW, 32>(vrs, voff + toff, slot + wave * NVW * 1024);
     };
     const uint16_t* klane = kring + lane * 8;  // this lane's 16 bytes in every K block
     const uint16_t* vlane = vring + lane * 4;  // this lane's 8 bytes in every V half-block
