@@ -822,14 +822,14 @@ struct GemmKernel {
       const bool nxt = ks_t >= ksteps;
       const uint32_t ks = (uint32_t)(nxt ? ks_t - ksteps : ks_t);
       const bool live = !nxt | has_next;
-      // (2^31 past the lane's offset is beyond every range: spans stay below 2 GiB)
+      // the slab offset moves the resource (range 0 when there is no slab): lane offsets stay fixed
       if constexpr (j < A_PER_WAVE) {
-        const uint32_t off = aoffs[j] + (live ? ks * a_slab_bytes : 0x80000000u);
-        buffer_load16_to_lds(a_rsrc(nxt ? m0n : m0c), off, slotb + (wave * A_PER_WAVE + j) * 1024);
+        buffer_load16_to_lds(slab_rsrc(a_rsrc(nxt ? m0n : m0c), ks * a_slab_bytes, live), aoffs[j],
+                             slotb + (wave * A_PER_WAVE + j) * 1024);
       } else {
         constexpr int jb = j - A_PER_WAVE;
-        const uint32_t off = boffs[jb] + (live ? ks * b_slab_bytes : 0x80000000u);
-        buffer_load16_to_lds(b_rsrc(nxt ? n0n : n0c), off, slotb + A_BYTES + (wave * B_PER_WAVE + jb) * 1024);
+        buffer_load16_to_lds(slab_rsrc(b_rsrc(nxt ? n0n : n0c), ks * b_slab_bytes, live), boffs[jb],
+                             slotb + A_BYTES + (wave * B_PER_WAVE + jb) * 1024);
       }
     };
 
